@@ -1,0 +1,700 @@
+// Flash-attention backward for gfx950 (CDNA4): dQ, dK, dV and a deterministic dBias.
+//
+// Semantics follow the reference's VoltaMmaBwd (cuda/volta_mma_attn_bwd.cu:84-451): P is rebuilt
+// from the forward's log2-domain lse, p = exp2(s2 - lse2); a dead logit (masked key, or a query
+// or key past the end) takes the masked logit -1e4, so P still carries dV for a masked key, while
+// dS = p (dP - delta) is zero there; delta = rowsum(out * dout) in fp32 from the fp16 tensors
+// (cuda/volta_attn_bwd.h:21-42); P and dS are fp16 before their GEMMs; dq = scale dS K and
+// dk = scale dS^T Q accumulate in fp32 and round once; dbias = sum over the N rows of dS in fp32,
+// unscaled, and all zeros without want_dbias (volta_mma_attn_bwd.cu:363).
+//
+// Where the reference adds dQ and dBias with fp32 atomics into global memory, this backward is
+// three kernels with no atomics, so every result is bit-identical from run to run:
+//   dq_kernel     one workgroup per (n, h, 128 queries), looping over key tiles as the forward
+//                 does: dQ^T = K^T dS^T accumulates in registers; it also writes delta.
+//   dkdv_kernel   one workgroup per (h, 64 keys, chunk of batch rows): for each row n of its
+//                 chunk it loops over query tiles, dV^T = dO^T P and dK^T = Q^T dS accumulate in
+//                 registers, and each wave adds its 16 keys' dS into an fp32 [64 keys][Sq] dBias
+//                 partial that stays in LDS for the whole chunk (one owner per element, fixed
+//                 order). The chunk's partial goes to the workspace once.
+//   dbias_kernel  dbias = the chunk partials summed in chunk order, transposed to [H,Sq,Sk].
+#include "clk_common.h"
+
+namespace clk {
+
+struct BwdArgs {
+    const half_t* q;
+    const half_t* k;
+    const half_t* v;
+    const half_t* bias;
+    const uint8_t* kmask;
+    const half_t* out;
+    const half_t* dout;
+    const float* lse;
+    half_t* dq;
+    half_t* dk;
+    half_t* dv;
+    float* dbias;
+    float* delta;    // workspace [N, H, Sq]
+    float* partial;  // workspace [chunks][H][kblocks][64][SqP]
+    int N, H, Sq, Sk, D;
+    int SqP;         // partial row stride (floats)
+    int kblocks;     // ceil(Sk / 64)
+    int chunk;       // batch rows per dkdv workgroup
+    int chunks;
+    float scale;
+    int bias_vec, mask_vec;
+};
+
+__device__ __forceinline__ half8 bzero8() {
+    half8 z;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) z[j] = (half_t)0.f;
+    return z;
+}
+
+__device__ __forceinline__ half8 bld8(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+
+struct BH16 {
+    half8 lo, hi;
+};
+
+__device__ __forceinline__ BH16 bload_h16(const half_t* p, int valid, bool vec) {
+    BH16 r;
+    if (vec && valid >= 16) {
+        r.lo = bld8(p);
+        r.hi = bld8(p + 8);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            r.lo[j] = j < valid ? p[j] : (half_t)0.f;
+            r.hi[j] = j + 8 < valid ? p[j + 8] : (half_t)0.f;
+        }
+    }
+    return r;
+}
+
+__device__ __forceinline__ uint4 bload_m16(const uint8_t* p, int valid, bool vec) {
+    if (vec && valid >= 16) return *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < valid) w[j / 4] |= (uint32_t)(p[j] != 0) << (8 * (j % 4));
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ uint32_t bmask_byte(const uint4& m, int key) {
+    const uint32_t w = key < 4 ? m.x : key < 8 ? m.y : key < 12 ? m.z : m.w;
+    return (w >> (8 * (key & 3))) & 0xffu;
+}
+
+// ------------------------------------------------------------------------------------------
+// dQ (and delta): the forward's orientation, S^T = K Q^T and dP^T = V dO^T with a lane on one
+// query; dQ^T = K^T dS^T takes dS^T straight from registers as its B operand.
+// ------------------------------------------------------------------------------------------
+template <int DP>
+struct DqTile {
+    static constexpr int kWaves = 4, kThreads = kWaves * kWave, kQB = 2;
+    static constexpr int kBQ = kWaves * kQB * 16, kBK = 64;
+    static constexpr int kKS = DP / 32, kDB = DP / 16;
+    static constexpr int kLd = DP + 8, kTLd = kBK + 8;
+    static constexpr int kChunks = kBK * DP / 8;
+    static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
+};
+
+template <int DP>
+__global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
+    using T = DqTile<DP>;
+    __shared__ __attribute__((aligned(16))) half_t Ks[T::kBK * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Vs[T::kBK * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Kt[DP * T::kTLd];
+
+    const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
+    const int item = xcd_item(blockIdx.x, gridDim.x);
+    const int qt = item % QT, rest = item / QT;
+    const int h = rest % a.H, n = rest / a.H;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int64_t nh = (int64_t)n * a.H + h;
+    const int64_t qbase = nh * a.Sq * a.D, kbase = nh * a.Sk * a.D;
+    const int q0w = qt * T::kBQ + wave * (T::kQB * 16);
+
+    // Q^T and dO^T B operands, lse2 and delta of this lane's queries
+    half8 qop[T::kQB][T::kKS], dop[T::kQB][T::kKS];
+    float lse2[T::kQB], dlt[T::kQB];
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        const int gq = q0w + 16 * qb + r16;
+        const bool in = gq < a.Sq;
+        float part = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < T::kKS; ++ks) {
+            const int d0 = 32 * ks + 8 * g;
+            const bool ok = in && d0 < a.D;
+            const int64_t off = qbase + (int64_t)gq * a.D + d0;
+            qop[qb][ks] = ok ? bld8(a.q + off) : bzero8();
+            dop[qb][ks] = ok ? bld8(a.dout + off) : bzero8();
+            const half8 o = ok ? bld8(a.out + off) : bzero8();
+#pragma unroll
+            for (int j = 0; j < 8; ++j) part += (float)o[j] * (float)dop[qb][ks][j];
+        }
+        dlt[qb] = wave_xor_sum4(part);
+        lse2[qb] = in ? a.lse[nh * a.Sq + gq] : 0.f;
+        if (in && g == 0) a.delta[nh * a.Sq + gq] = dlt[qb];
+    }
+
+    float4v acc[T::kDB][T::kQB];
+#pragma unroll
+    for (int db = 0; db < T::kDB; ++db)
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    half8 kreg[T::kCPT], vreg[T::kCPT];
+    const auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < T::kCPT; ++i) {
+            const int c = tid + i * T::kThreads;
+            const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
+            const bool ok = c < T::kChunks && k0 + row < a.Sk && col < a.D;
+            const int64_t off = kbase + (int64_t)(k0 + row) * a.D + col;
+            kreg[i] = ok ? bld8(a.k + off) : bzero8();
+            vreg[i] = ok ? bld8(a.v + off) : bzero8();
+        }
+    };
+    const auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < T::kCPT; ++i) {
+            const int c = tid + i * T::kThreads;
+            if (c < T::kChunks) {
+                const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
+                *reinterpret_cast<half8*>(&Ks[row * T::kLd + col]) = kreg[i];
+                *reinterpret_cast<half8*>(&Vs[row * T::kLd + col]) = vreg[i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) Kt[(col + j) * T::kTLd + row] = kreg[i][j];
+            }
+        }
+    };
+
+    const float scale = a.scale;
+    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
+    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
+
+    if (a.Sk > 0) fetch(0);
+    for (int k0 = 0; k0 < a.Sk; k0 += T::kBK) {
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (k0 + T::kBK < a.Sk) fetch(k0 + T::kBK);
+
+        const int kl = k0 + 16 * g;
+        const int kvalid = a.Sk - kl;
+        BH16 bias16[T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const int gq = q0w + 16 * qb + r16;
+            const int gqc = gq < a.Sq ? gq : a.Sq - 1;
+            bias16[qb] = bload_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
+        }
+        const uint4 mk = bload_m16(mrow + kl, kvalid, a.mask_vec);
+
+        float4v s[4][T::kQB], dp[4][T::kQB];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const int krow = 16 * (r16 >> 2) + 4 * kb + (r16 & 3);
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) {
+                s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                dp[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int ks = 0; ks < T::kKS; ++ks) {
+                const half8 kop = bld8(&Ks[krow * T::kLd + 32 * ks + 8 * g]);
+                const half8 vop = bld8(&Vs[krow * T::kLd + 32 * ks + 8 * g]);
+#pragma unroll
+                for (int qb = 0; qb < T::kQB; ++qb) {
+                    s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
+                    dp[kb][qb] = mfma16x16x32(vop, dop[qb][ks], dp[kb][qb]);
+                }
+            }
+        }
+
+        // dS^T = P^T (dP^T - delta), zero on a dead logit; packed as the B operand of dQ^T
+        half8 dsb[2][T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const int gq = q0w + 16 * qb + r16;
+            const bool qin = gq < a.Sq;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int kk = 4 * kb + i;
+                    const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
+                    const bool alive = qin && kk < kvalid && bmask_byte(mk, kk) != 0u;
+                    const float t = fmaf(s[kb][qb][i], scale, (float)b);
+                    const float p = exp2_fast(fmaf(t, kLog2e, -lse2[qb]));
+                    const float ds = pin_f32(alive ? p * (dp[kb][qb][i] - dlt[qb]) : 0.f);
+                    dsb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)ds;
+                }
+            }
+        }
+
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int db = 0; db < T::kDB; ++db) {
+                const int drow = (DP / 4) * (r16 >> 2) + 4 * db + (r16 & 3);
+                const half8 kto = bld8(&Kt[drow * T::kTLd + 16 * g + 8 * kt]);
+#pragma unroll
+                for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[kt][qb], acc[db][qb]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        const int gq = q0w + 16 * qb + r16;
+        if (gq >= a.Sq) continue;
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c) {
+            const int d0 = (DP / 4) * g + 8 * c;
+            if (d0 >= a.D) continue;
+            half8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[2 * c + j / 4][qb][j & 3] * scale);
+            *reinterpret_cast<half8*>(a.dq + qbase + (int64_t)gq * a.D + d0) = o;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// dK, dV and the dBias partials: S = Q K^T and dP = dO V^T with a lane on one key, so P and dS
+// feed dV^T = dO^T P and dK^T = Q^T dS as B operands straight from registers.
+// ------------------------------------------------------------------------------------------
+template <int DP>
+struct DkdvTile {
+    static constexpr int kWaves = 4, kThreads = kWaves * kWave;
+    static constexpr int kBK = kWaves * 16;   // keys per workgroup, 16 per wave
+    static constexpr int kBQ = 32;            // queries per tile (one contraction step)
+    static constexpr int kKS = DP / 32, kDB = DP / 16;
+    static constexpr int kLd = DP + 8, kTLd = kBQ + 8;
+    static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO
+    static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kStaticLds = (2 * kBQ * kLd + 2 * DP * kTLd) * 2;
+};
+
+template <int DP, bool DBIAS>
+__global__ __launch_bounds__(DkdvTile<DP>::kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
+    using T = DkdvTile<DP>;
+    __shared__ __attribute__((aligned(16))) half_t Qs[T::kBQ * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Os[T::kBQ * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Qt[DP * T::kTLd];
+    __shared__ __attribute__((aligned(16))) half_t Ot[DP * T::kTLd];
+    extern __shared__ __attribute__((aligned(16))) float DBt[];  // [kBK][SqP]
+
+    const int item = xcd_item(blockIdx.x, gridDim.x);
+    const int kblk = item % a.kblocks, rest = item / a.kblocks;
+    const int h = rest % a.H, c = rest / a.H;
+    const int n_begin = c * a.chunk;
+    const int n_end = min(a.N, n_begin + a.chunk);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int klocal = wave * 16 + r16;
+    const int key = kblk * T::kBK + klocal;
+    const bool kin = key < a.Sk;
+    const int qtiles = (a.Sq + T::kBQ - 1) / T::kBQ;
+
+    if constexpr (DBIAS) {
+        for (int i = tid; i < T::kBK * a.SqP; i += T::kThreads) DBt[i] = 0.f;
+    }
+
+    // Q / dO tile chunks, one tile ahead
+    half8 reg[T::kCPT];
+    const auto fetch = [&](int t) {
+        const int n = n_begin + t / qtiles, q0 = (t % qtiles) * T::kBQ;
+        const int64_t base = ((int64_t)n * a.H + h) * a.Sq * a.D;
+#pragma unroll
+        for (int i = 0; i < T::kCPT; ++i) {
+            const int cc = tid + i * T::kThreads;
+            const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
+            const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
+            const bool ok = cc < T::kChunks && q0 + row < a.Sq && col < a.D;
+            const half_t* src = which ? a.dout : a.q;
+            reg[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
+        }
+    };
+    const auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < T::kCPT; ++i) {
+            const int cc = tid + i * T::kThreads;
+            if (cc < T::kChunks) {
+                const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
+                const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
+                half_t* rm = which ? Os : Qs;
+                half_t* tr = which ? Ot : Qt;
+                *reinterpret_cast<half8*>(&rm[row * T::kLd + col]) = reg[i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) tr[(col + j) * T::kTLd + row] = reg[i][j];
+            }
+        }
+    };
+
+    const float scale = a.scale;
+    const float dead_logit = kMaskedLogit * kLog2e;
+    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
+    const int total = (n_end - n_begin) * qtiles;
+
+    half8 kop[T::kKS], vop[T::kKS];
+    bool kalive = false;
+    float4v accv[T::kDB], acck[T::kDB];
+
+    if (total > 0) fetch(0);
+    for (int t = 0; t < total; ++t) {
+        const int n = n_begin + t / qtiles, qi = t % qtiles, q0 = qi * T::kBQ;
+        const int64_t nh = (int64_t)n * a.H + h;
+        if (qi == 0) {
+            // this row's K and V as the B operands, lane column = key, slots d = 32 ks + 8 g + j
+            const int64_t kbase = nh * a.Sk * a.D;
+#pragma unroll
+            for (int ks = 0; ks < T::kKS; ++ks) {
+                const int d0 = 32 * ks + 8 * g;
+                const bool ok = kin && d0 < a.D;
+                kop[ks] = ok ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
+                vop[ks] = ok ? bld8(a.v + kbase + (int64_t)key * a.D + d0) : bzero8();
+            }
+            kalive = kin && a.kmask[(int64_t)n * a.Sk + key] != 0;
+#pragma unroll
+            for (int db = 0; db < T::kDB; ++db) {
+                accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
+                acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (t + 1 < total) fetch(t + 1);
+
+        // queries q0 + 8 g + j of this lane: their lse2, delta and bias at this lane's key
+        float l2[8], dl[8], bb[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int gq = q0 + 8 * g + j;
+            const bool in = gq < a.Sq;
+            l2[j] = in ? a.lse[nh * a.Sq + gq] : 0.f;
+            dl[j] = in ? a.delta[nh * a.Sq + gq] : 0.f;
+            bb[j] = (in && kin) ? (float)a.bias[bias_h + (int64_t)gq * a.Sk + key] : 0.f;
+        }
+
+        // S and dP: A row r of query block qb is query 8 (r/4) + 4 qb + r%4 of the tile
+        float4v s[2], dp[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qrow = 8 * (r16 >> 2) + 4 * qb + (r16 & 3);
+            s[qb] = float4v{0.f, 0.f, 0.f, 0.f};
+            dp[qb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < T::kKS; ++ks) {
+                const half8 qa = bld8(&Qs[qrow * T::kLd + 32 * ks + 8 * g]);
+                const half8 oa = bld8(&Os[qrow * T::kLd + 32 * ks + 8 * g]);
+                s[qb] = mfma16x16x32(qa, kop[ks], s[qb]);
+                dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
+            }
+        }
+
+        // lane holds query q0 + 8 g + 4 qb + i of its key: slot j = 4 qb + i
+        half8 pb, dsb;
+        float dsf[8];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = 4 * qb + i;
+                const bool alive = kalive && q0 + 8 * g + j < a.Sq;
+                const float s2 = alive ? fmaf(s[qb][i], scale, bb[j]) * kLog2e : dead_logit;
+                const float p = exp2_fast(s2 - l2[j]);
+                const float ds = pin_f32(alive ? p * (dp[qb][i] - dl[j]) : 0.f);
+                pb[j] = (half_t)p;
+                dsb[j] = (half_t)ds;
+                dsf[j] = ds;
+            }
+        }
+
+        // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4
+#pragma unroll
+        for (int db = 0; db < T::kDB; ++db) {
+            const int drow = (DP / 4) * (r16 >> 2) + 4 * db + (r16 & 3);
+            const half8 ot = bld8(&Ot[drow * T::kTLd + 8 * g]);
+            const half8 qt = bld8(&Qt[drow * T::kTLd + 8 * g]);
+            accv[db] = mfma16x16x32(ot, pb, accv[db]);
+            acck[db] = mfma16x16x32(qt, dsb, acck[db]);
+        }
+
+        if constexpr (DBIAS) {
+            float* row = DBt + klocal * a.SqP + q0 + 8 * g;
+            float4 lo = *reinterpret_cast<float4*>(row);
+            float4 hi = *reinterpret_cast<float4*>(row + 4);
+            lo.x += dsf[0]; lo.y += dsf[1]; lo.z += dsf[2]; lo.w += dsf[3];
+            hi.x += dsf[4]; hi.y += dsf[5]; hi.z += dsf[6]; hi.w += dsf[7];
+            *reinterpret_cast<float4*>(row) = lo;
+            *reinterpret_cast<float4*>(row + 4) = hi;
+        }
+
+        if (qi == qtiles - 1 && kin) {
+            // lane holds d = (DP/4) g .. +DP/4 of its key
+            const int64_t off = nh * a.Sk * a.D + (int64_t)key * a.D;
+#pragma unroll
+            for (int cc = 0; cc < DP / 32; ++cc) {
+                const int d0 = (DP / 4) * g + 8 * cc;
+                if (d0 >= a.D) continue;
+                half8 ok, ov;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
+                    ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
+                }
+                *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
+                *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
+            }
+        }
+    }
+
+    if constexpr (DBIAS) {
+        __syncthreads();
+        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * T::kBK * a.SqP;
+        for (int i = tid * 4; i < T::kBK * a.SqP; i += T::kThreads * 4) {
+            *reinterpret_cast<float4*>(dst + i) = *reinterpret_cast<const float4*>(DBt + i);
+        }
+    }
+}
+
+// dbias[h][q][64 kblk + kk] = sum over chunks, in chunk order, of partial[c][h][kblk][kk][q]
+__global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(BwdArgs a) {
+    __shared__ float tile[64][65];
+    const int qtiles = (a.Sq + 63) / 64;
+    const int item = blockIdx.x;
+    const int qt = item % qtiles, rest = item / qtiles;
+    const int kblk = rest % a.kblocks, h = rest / a.kblocks;
+    const int tid = threadIdx.x;
+    const int q0 = qt * 64;
+    {
+        const int kk = tid / 4, qc = (tid % 4) * 16;
+        float sum[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sum[j] = 0.f;
+        for (int c = 0; c < a.chunks; ++c) {
+            const float* src = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * 64 * a.SqP +
+                               (int64_t)kk * a.SqP + q0 + qc;
+#pragma unroll
+            for (int j = 0; j < 16; j += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(src + j);
+                sum[j] += v4.x;
+                sum[j + 1] += v4.y;
+                sum[j + 2] += v4.z;
+                sum[j + 3] += v4.w;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) tile[kk][qc + j] = sum[j];
+    }
+    __syncthreads();
+    {
+        const int qq = tid / 4, kc = (tid % 4) * 16;
+        const int gq = q0 + qq;
+        if (gq < a.Sq) {
+            float* dst = a.dbias + ((int64_t)h * a.Sq + gq) * a.Sk + kblk * 64;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                if (kblk * 64 + kc + j < a.Sk) dst[kc + j] = tile[kc + j][qq];
+            }
+        }
+    }
+}
+
+__global__ void fill_zero_f32(float* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        p[i] = 0.f;
+    }
+}
+
+// ---- host side ----------------------------------------------------------------------------
+
+static int cu_count(int device) {
+    static int cache[16] = {};
+    if (device < 0 || device >= 16) return 256;
+    if (cache[device] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+            v <= 0) {
+            v = 256;
+        }
+        cache[device] = v;
+    }
+    return cache[device];
+}
+
+struct BwdPlan {
+    int DP = 32;
+    int SqP = 0, kblocks = 0, chunk = 0, chunks = 0;
+    size_t dyn_lds = 0;
+    size_t delta_bytes = 0, partial_bytes = 0;
+    std::string error;
+};
+
+static size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
+
+static int dkdv_static_lds(int DP) {
+    return DP == 32 ? DkdvTile<32>::kStaticLds
+                    : DP == 64 ? DkdvTile<64>::kStaticLds : DkdvTile<96>::kStaticLds;
+}
+
+static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
+    BwdPlan p;
+    p.DP = D <= 32 ? 32 : D <= 64 ? 64 : 96;
+    // rows cover whole 64-query tiles of the reduce kernel; +4 floats staggers LDS banks
+    p.SqP = (int)(((Sq + 63) / 64) * 64 + 4);
+    p.kblocks = (int)((Sk + 63) / 64);
+    p.dyn_lds = (size_t)64 * p.SqP * sizeof(float);
+    const int limit = shared_limit(device);
+    const size_t per_wg = p.dyn_lds + dkdv_static_lds(p.DP);
+    if (limit > 0 && per_wg > (size_t)limit) {
+        p.error = "attention_bwd: dbias needs " + std::to_string(per_wg / 1024) +
+                  " KB shared, device allows " + std::to_string(limit / 1024) + " KB";
+    }
+    // enough workgroups to fill the chip once at the occupancy LDS allows
+    const int per_cu = limit > 0 ? std::max(1, std::min(4, (int)(limit / std::max<size_t>(per_wg, 1)))) : 1;
+    const int64_t target = (int64_t)cu_count(device) * per_cu;
+    const int64_t cols = H * p.kblocks;
+    int64_t chunks = cols > 0 ? std::max<int64_t>(1, target / cols) : 1;
+    chunks = std::min<int64_t>(chunks, std::max<int64_t>(N, 1));
+    p.chunk = (int)((N + chunks - 1) / std::max<int64_t>(chunks, 1));
+    if (p.chunk <= 0) p.chunk = 1;
+    p.chunks = (int)((N + p.chunk - 1) / p.chunk);
+    p.delta_bytes = round256((size_t)N * H * Sq * sizeof(float));
+    p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * 64 * p.SqP * sizeof(float));
+    return p;
+}
+
+template <int DP>
+static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bool want_dbias) {
+    using Q = DqTile<DP>;
+    const int64_t qt = (a.Sq + Q::kBQ - 1) / Q::kBQ;
+    const int64_t g1 = qt * a.H * a.N;
+    if (g1 > INT32_MAX) return invalid("attention_bwd: too many work items");
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
+    const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks;
+    if (want_dbias) {
+        if (p.dyn_lds > 64 * 1024) {
+            // LDS past 64 KB per workgroup is opt-in on some runtimes; failure shows at launch
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DP, true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.dyn_lds);
+        }
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, true>), dim3((unsigned)g2),
+                           dim3(DkdvTile<DP>::kThreads), p.dyn_lds, stream, a);
+        const int64_t g3 = (int64_t)((a.Sq + 63) / 64) * p.kblocks * a.H;
+        hipLaunchKernelGGL(attn_bwd_dbias_kernel, dim3((unsigned)g3), dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, false>), dim3((unsigned)g2),
+                           dim3(DkdvTile<DP>::kThreads), 0, stream, a);
+        const int64_t nb = (int64_t)a.H * a.Sq * a.Sk;
+        hipLaunchKernelGGL(fill_zero_f32, dim3(1024), dim3(256), 0, stream, a.dbias, nb);
+    }
+    return launch_status("attention_bwd");
+}
+
+static bool bwd_head_dim_ok(int64_t d) {
+    return d == 8 || d == 16 || d == 24 || d == 32 || d == 48 || d == 64 || d == 96;
+}
+
+}  // namespace clk
+
+using namespace clk;
+
+extern "C" size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buffer* q,
+                                                   const clk_buffer* k) {
+    if (q == nullptr || k == nullptr || q->rank != 4 || k->rank != 4) return 0;
+    const BwdPlan p = plan_bwd(device, q->dims[0], q->dims[1], q->dims[2], k->dims[2], q->dims[3]);
+    return p.delta_bytes + p.partial_bytes;
+}
+
+extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q,
+                                 const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
+                                 const clk_buffer* kmask, const clk_buffer* out,
+                                 const clk_buffer* dout, const clk_buffer* lse,
+                                 const clk_buffer* dq, const clk_buffer* dk, const clk_buffer* dv,
+                                 const clk_buffer* dbias, float scale, int32_t want_dbias,
+                                 void* workspace, size_t workspace_bytes) {
+    const clk_buffer* bufs[] = {q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias};
+    const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_U8,  CLK_F16,
+                         CLK_F16, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F32};
+    if (int st = check_types("attention_bwd", bufs, types, 12)) return st;
+    if (q->rank != 4) return invalid("q must be [N,H,S,D]");
+    const int64_t N = q->dims[0], H = q->dims[1], Sq = q->dims[2], D = q->dims[3];
+    if (k->rank != 4 || k->dims[0] != N || k->dims[1] != H || k->dims[3] != D) {
+        return invalid("volta_mma_bwd: k must be [N,H,Sk,D] like q");
+    }
+    const int64_t Sk = k->dims[2];
+    if (!same_shape(v, k) || !same_shape(dout, q)) {
+        return invalid("volta_mma_bwd: v must match k, dout must match q");
+    }
+    if (!dims_are(lse, N, H, Sq)) return invalid("volta_mma_bwd: lse must be [N,H,Sq]");
+    if (!same_shape(out, q)) return invalid("volta_mma_bwd: out must match q");
+    if (!dims_are(bias, H, Sq, Sk) || !dims_are(dbias, H, Sq, Sk)) {
+        return invalid("volta_mma_bwd: bias and dbias must be [H,Sq,Sk]");
+    }
+    if (!same_shape(dq, q) || !same_shape(dk, k) || !same_shape(dv, k)) {
+        return invalid("volta_mma_bwd: dq, dk, dv must match q, k, v");
+    }
+    if (elements(kmask) != N * Sk) return invalid("volta_mma_bwd: kmask must be [N,Sk]");
+    if (!bwd_head_dim_ok(D)) return invalid("volta_mma_bwd: unsupported head dim");
+    const void* vec[] = {q->data, k->data, v->data, out->data, dout->data, dq->data, dk->data, dv->data};
+    for (const void* p : vec) {
+        if (!aligned16(p)) return invalid("volta_mma_bwd: q, k, v, out, dout, dq, dk, dv must be 16-byte aligned");
+    }
+    const BwdPlan p = plan_bwd(device, N, H, Sq, Sk, D);
+    if (want_dbias && !p.error.empty()) return invalid(p.error);
+    if (N * H * Sq == 0 && H * Sq * Sk == 0) return ok();
+    const size_t need = p.delta_bytes + p.partial_bytes;
+    if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u)) {
+        return fail(CLK_INTERNAL, "volta_mma_bwd: the workspace must be 256-byte aligned and hold " +
+                                      std::to_string(need) + " bytes");
+    }
+    BwdArgs a{};
+    a.q = static_cast<const half_t*>(q->data);
+    a.k = static_cast<const half_t*>(k->data);
+    a.v = static_cast<const half_t*>(v->data);
+    a.bias = static_cast<const half_t*>(bias->data);
+    a.kmask = static_cast<const uint8_t*>(kmask->data);
+    a.out = static_cast<const half_t*>(out->data);
+    a.dout = static_cast<const half_t*>(dout->data);
+    a.lse = static_cast<const float*>(lse->data);
+    a.dq = static_cast<half_t*>(dq->data);
+    a.dk = static_cast<half_t*>(dk->data);
+    a.dv = static_cast<half_t*>(dv->data);
+    a.dbias = static_cast<float*>(dbias->data);
+    a.delta = static_cast<float*>(workspace);
+    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.delta_bytes);
+    a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
+    a.SqP = p.SqP;
+    a.kblocks = p.kblocks;
+    a.chunk = p.chunk;
+    a.chunks = p.chunks;
+    a.scale = scale;
+    a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
+    a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (N * H * Sq == 0 || Sk == 0) {
+        // nothing to differentiate: zero gradients (dk, dv keep their shape with Sk == 0)
+        const int64_t nq = N * H * Sq * D;
+        if (nq > 0) {
+            hipLaunchKernelGGL(fill_zero_f32, dim3(256), dim3(256), 0, s,
+                               static_cast<float*>(dq->data), nq / 2);
+        }
+        return launch_status("attention_bwd");
+    }
+    if (p.DP == 32) return launch_bwd<32>(s, a, p, want_dbias);
+    if (p.DP == 64) return launch_bwd<64>(s, a, p, want_dbias);
+    return launch_bwd<96>(s, a, p, want_dbias);
+}

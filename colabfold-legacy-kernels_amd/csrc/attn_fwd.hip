@@ -1,0 +1,508 @@
+// Biased, masked, optionally gated flash-attention forward for gfx950 (CDNA4).
+//
+// Semantics follow the reference's VoltaMma / VoltaMmaPacked / VoltaMmaPackedTrim
+// (cuda/volta_mma_attn.cu:115-465, 522-623): logits = scale q.k + bias[h,q,k] for a kept key,
+// the masked logit -1e4 for a masked key (bias ignored), -inf past Sk; online softmax with the
+// lazy max rule (the running max moves only when a tile raises it by more than 2^6 in the
+// exp2 domain, decided per wave); P rounded to fp16 for the P.V product while l sums the fp32
+// P; out = fp16(gate(O / max(l, 1e-30))); lse = m + log2 l in the log2 domain, -inf when l == 0.
+//
+// Layout on the chip. A workgroup is 4 waves and 128 queries of one (n, h): each wave owns 32
+// queries as two 16-column MFMA blocks. Key tiles of 64 stream through LDS: K row-major (the A
+// operand of S^T = K Q^T) and V transposed (the A operand of O^T = V^T P^T). Working in the
+// transposed orientation keeps everything a lane touches on ONE query: the S^T accumulator of
+// lane l holds keys 16 (l/16) + 4 kb + i of query l % 16, so the softmax statistics and the
+// O rescale are per-lane scalars, P^T feeds the second MFMA as its B operand without leaving
+// registers, and a lane's bias and mask are 16 contiguous elements of one row.
+#include "clk_common.h"
+
+namespace clk {
+
+struct FwdArgs {
+    const half_t* q;
+    const half_t* k;
+    const half_t* v;
+    const half_t* bias;
+    const uint8_t* kmask;
+    half_t* out;
+    float* lse;
+    const half_t* gate;       // same strides as q (the packed form's fourth slot), or null
+    const half_t* gate_bias;  // [H, D]
+    const int32_t* lims;      // [N + 1] (trim), or null
+    int64_t qn, qh, qs, kn, kh, ks, on, oh, os;  // element strides of q/gate, k/v, out
+    int N, H, Sq, Sk, D;
+    float scale;
+    int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0)
+    int mask_vec;  // mask rows are whole 16-byte vectors (Sk % 16 == 0)
+};
+
+template <int DP>
+struct FwdTile {
+    static constexpr int kWaves = 4;
+    static constexpr int kThreads = kWaves * kWave;
+    static constexpr int kQB = 2;                     // 16-query MFMA blocks per wave
+    static constexpr int kBQ = kWaves * kQB * 16;     // queries per workgroup
+    static constexpr int kBK = 64;                    // keys per tile
+    static constexpr int kKS = DP / 32;               // contraction steps of S^T
+    static constexpr int kDB = DP / 16;               // 16-row blocks of O^T
+    static constexpr int kKsLd = DP + 8;              // K row stride in LDS (halfs)
+    static constexpr int kVtLd = kBK + 8;             // V^T row stride in LDS (halfs)
+    static constexpr int kChunks = kBK * DP / 8;      // 16-byte chunks in a K (or V) tile
+    static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kLds = (kBK * kKsLd + DP * kVtLd) * 2;
+};
+
+struct H16 {
+    half8 lo, hi;
+};
+
+__device__ __forceinline__ half8 zero8() {
+    half8 z;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) z[j] = (half_t)0.f;
+    return z;
+}
+
+__device__ __forceinline__ half8 ld8(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+
+// 16 consecutive halfs from p, elements at or past `valid` as 0
+__device__ __forceinline__ H16 load_h16(const half_t* p, int valid, bool vec) {
+    H16 r;
+    if (vec && valid >= 16) {
+        r.lo = ld8(p);
+        r.hi = ld8(p + 8);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            r.lo[j] = j < valid ? p[j] : (half_t)0.f;
+            r.hi[j] = j + 8 < valid ? p[j + 8] : (half_t)0.f;
+        }
+    }
+    return r;
+}
+
+// 16 consecutive mask bytes as four little-endian words, bytes at or past `valid` as 0
+__device__ __forceinline__ uint4 load_m16(const uint8_t* p, int valid, bool vec) {
+    if (vec && valid >= 16) return *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        if (j < valid) w[j / 4] |= (uint32_t)(p[j] != 0) << (8 * (j % 4));
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ bool all_bytes_set(uint32_t w) {
+    return ((w - 0x01010101u) & ~w & 0x80808080u) == 0u;
+}
+
+__device__ __forceinline__ uint32_t mask_byte(const uint4& m, int key) {
+    const uint32_t w = key < 4 ? m.x : key < 8 ? m.y : key < 12 ? m.z : m.w;
+    return (w >> (8 * (key & 3))) & 0xffu;
+}
+
+template <int DP, bool LSE, bool GATE, bool TRIM>
+__global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs a) {
+    using T = FwdTile<DP>;
+    __shared__ __attribute__((aligned(16))) half_t Ks[T::kBK * T::kKsLd];
+    __shared__ __attribute__((aligned(16))) half_t Vt[DP * T::kVtLd];
+
+    const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
+    const int item = xcd_item(blockIdx.x, gridDim.x);
+    const int qt = item % QT, rest = item / QT;
+    const int h = rest % a.H, n = rest / a.H;
+    const int q0 = qt * T::kBQ;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+
+    const int64_t qbase = n * a.qn + h * a.qh;
+    const int64_t kbase = n * a.kn + h * a.kh;
+    const int64_t obase = n * a.on + h * a.oh;
+
+    int k_end = a.Sk;
+    if constexpr (TRIM) {
+        // a row with no live key, or a query tile past every row's live keys, is padding
+        k_end = a.lims[n];
+        if (k_end == 0 || q0 >= a.lims[a.N]) {
+            const int cpr = a.D / 8;
+            for (int i = tid; i < T::kBQ * cpr; i += T::kThreads) {
+                const int r = i / cpr, c = (i - r * cpr) * 8, gq = q0 + r;
+                if (gq < a.Sq) {
+                    *reinterpret_cast<uint4*>(a.out + obase + gq * a.os + c) =
+                        make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
+            return;
+        }
+    }
+
+    // Q^T as the B operand of S^T: lane column q = q0w + 16 qb + r16, slots d = 32 ks + 8 g + j
+    const int q0w = q0 + wave * (T::kQB * 16);
+    half8 qop[T::kQB][T::kKS];
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        const int gq = q0w + 16 * qb + r16;
+#pragma unroll
+        for (int ks = 0; ks < T::kKS; ++ks) {
+            const int d0 = 32 * ks + 8 * g;
+            qop[qb][ks] = (gq < a.Sq && d0 < a.D) ? ld8(a.q + qbase + gq * a.qs + d0) : zero8();
+        }
+    }
+
+    float m_run[T::kQB], l_run[T::kQB];
+    float4v acc[T::kDB][T::kQB];
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        m_run[qb] = -INFINITY;
+        l_run[qb] = 0.f;
+#pragma unroll
+        for (int db = 0; db < T::kDB; ++db) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // K/V tile chunks held in registers one tile ahead of their LDS store
+    half8 kreg[T::kCPT], vreg[T::kCPT];
+    const auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < T::kCPT; ++i) {
+            const int c = tid + i * T::kThreads;
+            const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
+            const bool ok = c < T::kChunks && k0 + row < a.Sk && col < a.D;
+            const int64_t off = kbase + (int64_t)(k0 + row) * a.ks + col;
+            kreg[i] = ok ? ld8(a.k + off) : zero8();
+            vreg[i] = ok ? ld8(a.v + off) : zero8();
+        }
+    };
+    const auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < T::kCPT; ++i) {
+            const int c = tid + i * T::kThreads;
+            if (c < T::kChunks) {
+                const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
+                *reinterpret_cast<half8*>(&Ks[row * T::kKsLd + col]) = kreg[i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) Vt[(col + j) * T::kVtLd + row] = vreg[i][j];
+            }
+        }
+    };
+
+    const float scale = a.scale;
+    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
+    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
+
+    if (k_end > 0) fetch(0);
+    for (int k0 = 0; k0 < k_end; k0 += T::kBK) {
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (k0 + T::kBK < k_end) fetch(k0 + T::kBK);
+
+        // this lane's 16 keys k0 + 16 g .. +15: bias of its queries and the mask
+        const int kl = k0 + 16 * g;
+        const int kvalid = a.Sk - kl;
+        H16 bias16[T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const int gq = q0w + 16 * qb + r16;
+            const int gqc = gq < a.Sq ? gq : a.Sq - 1;
+            bias16[qb] = load_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
+        }
+        const uint4 mk = load_m16(mrow + kl, kvalid, a.mask_vec);
+        const bool kept = kvalid >= 16 && all_bytes_set(mk.x) && all_bytes_set(mk.y) &&
+                          all_bytes_set(mk.z) && all_bytes_set(mk.w);
+        const bool fast = __all(kept);
+
+        // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4
+        float4v s[4][T::kQB];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const int krow = 16 * (r16 >> 2) + 4 * kb + (r16 & 3);
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < T::kKS; ++ks) {
+                const half8 kop = ld8(&Ks[krow * T::kKsLd + 32 * ks + 8 * g]);
+#pragma unroll
+                for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
+            }
+        }
+
+        // natural-domain logits t = scale s + bias; masked keys -1e4, keys past Sk -inf
+        float m_tile[T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int kk = 4 * kb + i;
+                    const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
+                    float t = fmaf(s[kb][qb][i], scale, (float)b);
+                    if (!fast) {
+                        const bool in = kk < kvalid;
+                        t = (in && mask_byte(mk, kk) != 0u) ? t : (in ? kMaskedLogit : -INFINITY);
+                    }
+                    s[kb][qb][i] = t;
+                    mx = fmaxf(mx, t);
+                }
+            }
+            m_tile[qb] = wave_xor_max4(mx);
+        }
+
+        // lazy max: move only when some query of the wave gains more than 6 in log2 units
+        bool up = false;
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) up |= m_tile[qb] * kLog2e > m_run[qb] * kLog2e + 6.f;
+        const bool raise = __any(up);
+
+        half8 pb[2][T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const float m_new = raise ? fmaxf(m_run[qb], m_tile[qb]) : m_run[qb];
+            const float alpha = raise ? exp2_fast((m_run[qb] - m_new) * kLog2e) : 1.f;
+            const float nm2 = -m_new * kLog2e;
+            float lsum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = exp2_fast(fmaf(s[kb][qb][i], kLog2e, nm2));
+                    lsum += p;
+                    pb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)p;
+                }
+            }
+            l_run[qb] = l_run[qb] * alpha + lsum;
+            m_run[qb] = m_new;
+            if (raise) {
+#pragma unroll
+                for (int db = 0; db < T::kDB; ++db) acc[db][qb] *= alpha;
+            }
+        }
+
+        // O^T += V^T P^T: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4; slot 8 g + j of
+        // contraction step kt is key 16 g + 8 kt + j, which is where P^T already sits
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int db = 0; db < T::kDB; ++db) {
+                const int drow = (DP / 4) * (r16 >> 2) + 4 * db + (r16 & 3);
+                const half8 vop = ld8(&Vt[drow * T::kVtLd + 16 * g + 8 * kt]);
+#pragma unroll
+                for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(vop, pb[kt][qb], acc[db][qb]);
+            }
+        }
+    }
+
+    // epilogue: lane g holds d = (DP/4) g .. +DP/4 of query q0w + 16 qb + r16
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        const int gq = q0w + 16 * qb + r16;
+        const float l = wave_xor_sum4(l_run[qb]);
+        if (gq >= a.Sq) continue;
+        if constexpr (LSE) {
+            if (g == 0) {
+                a.lse[((int64_t)n * a.H + h) * a.Sq + gq] =
+                    l > 0.f ? m_run[qb] * kLog2e + log2f(l) : -INFINITY;
+            }
+        }
+        const float inv = 1.0f / fmaxf(l, 1e-30f);
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c) {
+            const int d0 = (DP / 4) * g + 8 * c;
+            if (d0 >= a.D) continue;
+            half8 o;
+            half8 gt, gb;
+            if constexpr (GATE) {
+                gt = ld8(a.gate + qbase + gq * a.qs + d0);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) gb[j] = a.gate_bias[h * a.D + d0 + j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int db = 2 * c + j / 4, i = j & 3;
+                float val = acc[db][qb][i] * inv;
+                if constexpr (GATE) val *= sigmoid_fast((float)gt[j] + (float)gb[j]);
+                o[j] = (half_t)val;
+            }
+            *reinterpret_cast<half8*>(a.out + obase + gq * a.os + d0) = o;
+        }
+    }
+}
+
+template <int DP, bool LSE, bool GATE, bool TRIM>
+static int launch_fwd(hipStream_t stream, int device, const FwdArgs& a) {
+    using T = FwdTile<DP>;
+    const int max_smem = shared_limit(device);
+    if (max_smem > 0 && T::kLds > max_smem) {
+        return invalid("attention: needs " + std::to_string(T::kLds / 1024) +
+                       " KB shared, device allows " + std::to_string(max_smem / 1024) + " KB");
+    }
+    const int64_t qt = (a.Sq + T::kBQ - 1) / T::kBQ;
+    const int64_t grid = qt * a.H * a.N;
+    if (grid == 0) return ok();
+    if (grid > INT32_MAX) return invalid("attention: too many work items");
+    hipLaunchKernelGGL((attn_fwd_kernel<DP, LSE, GATE, TRIM>), dim3((unsigned)grid),
+                       dim3(T::kThreads), 0, stream, a);
+    return launch_status("attention");
+}
+
+// The (D, block_q, block_k) entries the reference dispatches (volta_mma_attn.cu:508-517). The
+// gfx950 kernel picks its own tiling per D; the table keeps the FFI contract, so a call the
+// reference rejects is rejected here too.
+static bool fwd_config_ok(int64_t d, int64_t bq, int64_t bk) {
+    static const int64_t table[][3] = {
+        {8, 64, 64},  {8, 64, 32},  {8, 32, 32},  {8, 128, 64}, {8, 32, 64},  {32, 64, 64},
+        {32, 64, 32}, {32, 32, 64}, {32, 32, 32}, {32, 128, 64}, {32, 16, 64}, {16, 64, 64},
+        {16, 32, 32}, {16, 64, 32}, {64, 64, 64}, {64, 32, 32}, {24, 64, 32}, {24, 32, 32},
+        {48, 64, 32}, {48, 32, 32}, {96, 64, 32}, {96, 32, 32}};
+    for (const auto& e : table)
+        if (e[0] == d && e[1] == bq && e[2] == bk) return true;
+    return false;
+}
+
+template <bool LSE, bool GATE, bool TRIM>
+static int dispatch_fwd(hipStream_t stream, int device, const FwdArgs& a) {
+    if (a.D <= 32) return launch_fwd<32, LSE, GATE, TRIM>(stream, device, a);
+    if (a.D <= 64) return launch_fwd<64, LSE, GATE, TRIM>(stream, device, a);
+    return launch_fwd<96, LSE, GATE, TRIM>(stream, device, a);
+}
+
+static FwdArgs contiguous_args(int N, int H, int Sq, int Sk, int D) {
+    FwdArgs a{};
+    a.qn = (int64_t)H * Sq * D;
+    a.qh = (int64_t)Sq * D;
+    a.qs = D;
+    a.kn = (int64_t)H * Sk * D;
+    a.kh = (int64_t)Sk * D;
+    a.ks = D;
+    a.on = a.qn;
+    a.oh = a.qh;
+    a.os = D;
+    a.N = N;
+    a.H = H;
+    a.Sq = Sq;
+    a.Sk = Sk;
+    a.D = D;
+    return a;
+}
+
+}  // namespace clk
+
+using namespace clk;
+
+extern "C" int clk_attention_fwd(clk_stream stream, int32_t device, const clk_buffer* q,
+                                 const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
+                                 const clk_buffer* kmask, const clk_buffer* out,
+                                 const clk_buffer* lse, float scale, int64_t block_q,
+                                 int64_t block_k, int32_t want_lse) {
+    const clk_buffer* bufs[] = {q, k, v, bias, kmask, out, lse};
+    const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_U8, CLK_F16, CLK_F32};
+    if (int st = check_types("attention", bufs, types, 7)) return st;
+    if (q->rank != 4) return invalid("q must be [N,H,S,D]");
+    const int64_t N = q->dims[0], H = q->dims[1], Sq = q->dims[2], D = q->dims[3];
+    if (k->rank != 4 || k->dims[0] != N || k->dims[1] != H || k->dims[3] != D || !same_shape(v, k)) {
+        return invalid("attention: k and v must be [N,H,Sk,D] like q");
+    }
+    const int64_t Sk = k->dims[2];
+    if (!same_shape(out, q)) return invalid("attention: out must match q");
+    if (elements(bias) != H * Sq * Sk || elements(kmask) != N * Sk) {
+        return invalid("attention: bias must be [H,Sq,Sk] and kmask [N,Sk]");
+    }
+    if (want_lse && elements(lse) != N * H * Sq) return invalid("attention: lse must be [N,H,Sq]");
+    if (!fwd_config_ok(D, block_q, block_k)) return invalid("volta_mma: unsupported (D, bq, bk)");
+    if (!aligned16(q->data) || !aligned16(k->data) || !aligned16(v->data) || !aligned16(out->data)) {
+        return invalid("attention: q, k, v and out must be 16-byte aligned");
+    }
+    if (N * H * Sq == 0) return ok();
+    FwdArgs a = contiguous_args((int)N, (int)H, (int)Sq, (int)Sk, (int)D);
+    a.q = static_cast<const half_t*>(q->data);
+    a.k = static_cast<const half_t*>(k->data);
+    a.v = static_cast<const half_t*>(v->data);
+    a.bias = static_cast<const half_t*>(bias->data);
+    a.kmask = static_cast<const uint8_t*>(kmask->data);
+    a.out = static_cast<half_t*>(out->data);
+    a.lse = want_lse ? static_cast<float*>(lse->data) : nullptr;
+    a.scale = scale;
+    a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
+    a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return want_lse ? dispatch_fwd<true, false, false>(s, device, a)
+                    : dispatch_fwd<false, false, false>(s, device, a);
+}
+
+static int packed_common(clk_stream stream, int32_t device, const clk_buffer* p,
+                         const clk_buffer* bias, const clk_buffer* kmask,
+                         const clk_buffer* gate_bias, const clk_buffer* lims,
+                         const clk_buffer* out, float scale, int64_t block_q, int64_t block_k,
+                         int32_t column) {
+    const char* what = lims ? "attention_packed_trim" : "attention_packed";
+    const clk_buffer* bufs[] = {p, bias, kmask, gate_bias, out, lims};
+    const int types[] = {CLK_F16, CLK_F16, CLK_U8, CLK_F16, CLK_F16, CLK_S32};
+    if (int st = check_types(what, bufs, types, lims ? 6 : 5)) return st;
+    if (p->rank != 5 || (p->dims[2] != 3 && p->dims[2] != 4)) {
+        return invalid("p must be [X,Y,3 or 4,H,D]");
+    }
+    const int64_t X = p->dims[0], Y = p->dims[1], G = p->dims[2], H = p->dims[3], D = p->dims[4];
+    const int64_t N = column ? Y : X, S = column ? X : Y;
+    if (elements(bias) != H * S * S || elements(kmask) != N * S ||
+        (G == 4 && elements(gate_bias) != H * D)) {
+        return invalid("bias must be [H,S,S], kmask [N,S], gate_bias [H,D]");
+    }
+    if (elements(out) != X * Y * H * D) return invalid(std::string(what) + ": out must be [X,Y,H,D]");
+    if (lims && elements(lims) != N + 1) return invalid("attention_packed_trim: lims must be [N+1]");
+    if (!fwd_config_ok(D, block_q, block_k)) return invalid("volta_mma: unsupported (D, bq, bk)");
+    if (!aligned16(p->data) || !aligned16(out->data)) {
+        return invalid(std::string(what) + ": p and out must be 16-byte aligned");
+    }
+    if (N * H * S == 0) return ok();
+    const half_t* pp = static_cast<const half_t*>(p->data);
+    FwdArgs a{};
+    const int64_t pn = G * H * D, pr = Y * pn, on = H * D, orow = Y * on;
+    if (column) {
+        a.qn = pn; a.qh = D; a.qs = pr;
+        a.on = on; a.oh = D; a.os = orow;
+    } else {
+        a.qn = pr; a.qh = D; a.qs = pn;
+        a.on = orow; a.oh = D; a.os = on;
+    }
+    a.kn = a.qn; a.kh = a.qh; a.ks = a.qs;
+    a.N = (int)N; a.H = (int)H; a.Sq = (int)S; a.Sk = (int)S; a.D = (int)D;
+    a.q = pp;
+    a.k = pp + H * D;
+    a.v = pp + 2 * H * D;
+    a.gate = G == 4 ? pp + 3 * H * D : nullptr;
+    a.gate_bias = G == 4 ? static_cast<const half_t*>(gate_bias->data) : nullptr;
+    a.lims = lims ? static_cast<const int32_t*>(lims->data) : nullptr;
+    a.bias = static_cast<const half_t*>(bias->data);
+    a.kmask = static_cast<const uint8_t*>(kmask->data);
+    a.out = static_cast<half_t*>(out->data);
+    a.lse = nullptr;
+    a.scale = scale;
+    a.bias_vec = S % 8 == 0 && aligned16(a.bias);
+    a.mask_vec = S % 16 == 0 && aligned16(a.kmask);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (lims) {
+        return G == 4 ? dispatch_fwd<false, true, true>(s, device, a)
+                      : dispatch_fwd<false, false, true>(s, device, a);
+    }
+    return G == 4 ? dispatch_fwd<false, true, false>(s, device, a)
+                  : dispatch_fwd<false, false, false>(s, device, a);
+}
+
+extern "C" int clk_attention_packed(clk_stream stream, int32_t device, const clk_buffer* p,
+                                    const clk_buffer* bias, const clk_buffer* kmask,
+                                    const clk_buffer* gate_bias, const clk_buffer* out, float scale,
+                                    int64_t block_q, int64_t block_k, int32_t column) {
+    return packed_common(stream, device, p, bias, kmask, gate_bias, nullptr, out, scale, block_q,
+                         block_k, column);
+}
+
+extern "C" int clk_attention_packed_trim(clk_stream stream, int32_t device, const clk_buffer* p,
+                                         const clk_buffer* bias, const clk_buffer* kmask,
+                                         const clk_buffer* gate_bias, const clk_buffer* lims,
+                                         const clk_buffer* out, float scale, int64_t block_q,
+                                         int64_t block_k, int32_t column) {
+    if (lims == nullptr) return invalid("attention_packed_trim: lims is missing");
+    return packed_common(stream, device, p, bias, kmask, gate_bias, lims, out, scale, block_q,
+                         block_k, column);
+}

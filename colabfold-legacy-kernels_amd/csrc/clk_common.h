@@ -1,0 +1,112 @@
+// Shared types and helpers of the gfx950 ColabFold kernels: MFMA operand types, status
+// reporting, buffer validation and the XCD-aware work-item mapping.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "colabfold_gfx950.h"
+
+namespace clk {
+
+// ---- device side --------------------------------------------------------------------------
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// A masked key's logit, replacing its biased score (the reference's AlphaFold fp16 mask bias):
+// -inf would leave inf - inf on a row whose keys are all masked (cuda/volta_attn.h:9-11).
+constexpr float kMaskedLogit = -1.0e4f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// One v_mfma_f32_16x16x32_f16: D[16x16] += A[16x32] B[32x16], fp32 accumulate. Lane l supplies
+// A row (l % 16) and B column (l % 16), eight contraction slots each (slot group l / 16), and
+// holds D rows 4 (l / 16) .. +3 of column l % 16.
+__device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Pin v as an fp32 register value, so its later rounding to fp16 is a separate step that the
+// compiler cannot fold into the multiply producing v (v_fma_mixlo_f16 rounds once). Every
+// template variant of a kernel then rounds alike, as the reference rounds its fp32 dS.
+__device__ __forceinline__ float pin_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// sigmoid(g) = 1 / (1 + 2^(-g log2 e)), one v_exp_f32 and one v_rcp_f32
+__device__ __forceinline__ float sigmoid_fast(float g) {
+    return __builtin_amdgcn_rcpf(1.0f + exp2_fast(-kLog2e * g));
+}
+
+__device__ __forceinline__ float wave_xor_sum4(float v) {
+    // sum over the four lanes l, l^16, l^32, l^48 (one MFMA column's row groups)
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ float wave_xor_max4(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+// Work item of a 1-D launch, with consecutive items on the same XCD: the dispatcher deals
+// workgroups round-robin over the 8 XCDs, so item i of XCD x is slot x's i-th workgroup.
+// Neighbouring items share K/V (or weights) through that XCD's L2.
+__device__ __forceinline__ int xcd_item(int linear, int count) {
+    constexpr int kXcds = 8;
+    const int x = linear % kXcds, s = linear / kXcds;
+    const int per = count / kXcds, extra = count % kXcds;
+    return x * per + (x < extra ? x : extra) + s;
+}
+
+// ---- host side ----------------------------------------------------------------------------
+
+// Thread-local last error; every entry point returns through ok() or fail().
+int fail(int code, const std::string& msg);
+int ok();
+
+inline int invalid(const std::string& msg) { return fail(CLK_INVALID_ARGUMENT, msg); }
+
+int launch_status(const char* what);
+
+// Device LDS limit per workgroup, read once per device (a benign race, like the reference's
+// per-device caches).
+int shared_limit(int device);
+
+inline int64_t elements(const clk_buffer* b) {
+    int64_t n = 1;
+    for (int i = 0; i < b->rank; ++i) n *= b->dims[i];
+    return n;
+}
+
+inline bool is_rank(const clk_buffer* b, int r) { return b != nullptr && b->rank == r; }
+
+inline bool same_shape(const clk_buffer* a, const clk_buffer* b) {
+    if (a->rank != b->rank) return false;
+    for (int i = 0; i < a->rank; ++i)
+        if (a->dims[i] != b->dims[i]) return false;
+    return true;
+}
+
+inline bool dims_are(const clk_buffer* b, int64_t d0, int64_t d1, int64_t d2) {
+    return b->rank == 3 && b->dims[0] == d0 && b->dims[1] == d1 && b->dims[2] == d2;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The element-type check XLA's typed binding does before the handler runs.
+int check_types(const char* what, const clk_buffer* const* bufs, const int* types, int n);
+
+}  // namespace clk

@@ -1,0 +1,1035 @@
+// LayerNorm-fused pair-stack projections for gfx950 (CDNA4): ln_gdp, trimul_epilogue,
+// ln_projection, output_projection and transition.
+//
+// Semantics follow the reference (cuda/volta_ops.cu:330-641, cuda/volta_gdp.h, FFI validation in
+// cuda/volta_fused_ffi.h:16-259): LayerNorm with two-pass fp32 statistics and its output rounded
+// to fp16 before the GEMM; fp16 operands with fp32 accumulation; sigmoid gates; the transition's
+// hidden activation rounded to fp16; keep decisions per row tile of 64 (32 for the tri-mul
+// epilogue and the 256-channel transition), rows past M counting as `other`.
+//
+// Layout on the chip. Workgroups are persistent (a grid of about one per CU, each looping over
+// row tiles), so a layer's weights are read from HBM once per workgroup and then stay in LDS.
+// Every matrix in LDS is stored "fragment-major": for operand block b and contraction step ks,
+// the 64 lanes' 16-byte MFMA operands are 64 consecutive chunks, so a wave's operand read is one
+// conflict-free 1 KB sweep and no row padding is needed (which is what lets a 512 x 128 weight
+// and a 64-row activation tile share one CU's 160 KB). Row-major results use the transposed
+// product out^T = W X^T, whose accumulator gives a lane 8 consecutive columns of one row (a
+// 16-byte store); channel-major results use out = X W^T, giving a lane 16 consecutive rows of
+// one channel.
+#include "clk_common.h"
+
+namespace clk {
+
+constexpr int kFThreads = 256;
+constexpr int kFWaves = kFThreads / kWave;
+constexpr int kTileRows = 64;
+
+enum TileWork { kCompute = 0, kPadding = 1, kSkip = 2 };
+
+__device__ __forceinline__ half8 fzero8() {
+    half8 z;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) z[j] = (half_t)0.f;
+    return z;
+}
+__device__ __forceinline__ half8 fld8(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+__device__ __forceinline__ void fst8(half_t* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
+
+// operand chunk (block, step, lane) of a fragment-major matrix with KS contraction steps
+__device__ __forceinline__ int frag(int block, int ks, int KS, int lane) {
+    return ((block * KS + ks) * kWave + lane) * 8;
+}
+
+// A-operand row r of block b for a transposed product: blocks pair up so that the accumulator
+// gives lane group g the 8 consecutive outputs 32 (b/2) + 8 g .. +7
+__device__ __forceinline__ int pair_row(int b, int r) {
+    return 32 * (b >> 1) + 8 * (r >> 2) + 4 * (b & 1) + (r & 3);
+}
+
+// A-operand row r of row block rb for a channel-major product: lane group g then holds the 16
+// consecutive rows 16 g .. +15 across the four row blocks
+__device__ __forceinline__ int quad_row(int rb, int r) { return 16 * (r >> 2) + 4 * rb + (r & 3); }
+
+// What a row tile does, with the reference's rule (cuda/volta_gdp.h:114-136): compute when a
+// keep is above zero, write padding when all are at most zero and one is zero, skip otherwise.
+// Rows at or past M read as `other`. Every thread of the block must call it.
+__device__ __forceinline__ int tile_work(const half_t* keep, int M, int m0, int R, float other) {
+    if (keep == nullptr) return kCompute;
+    bool live = false, zero = false;
+    for (int r = threadIdx.x; r < R; r += blockDim.x) {
+        const float k = m0 + r < M ? (float)keep[m0 + r] : other;
+        live |= k > 0.f;
+        zero |= k == 0.f;
+    }
+    if (__syncthreads_or(live)) return kCompute;
+    return __syncthreads_or(zero) ? kPadding : kSkip;
+}
+
+// Weight rows [0, rows) of a row-major [rows][K] fp16 matrix into fragment-major LDS, nblocks
+// blocks of 16 rows; PAIRED uses pair_row, otherwise block b holds rows 16 b .. +15. Rows past
+// `rows` are zero.
+template <int K, bool PAIRED>
+__device__ __forceinline__ void load_weight_frags(half_t* dst, const half_t* W, int rows, int nblocks,
+                                                  int row0 = 0) {
+    constexpr int KS = K / 32;
+    for (int i = threadIdx.x; i < nblocks * KS * kWave; i += blockDim.x) {
+        const int lane = i % kWave, t = i / kWave, ks = t % KS, b = t / KS;
+        const int r = PAIRED ? pair_row(b, lane & 15) : 16 * b + (lane & 15);
+        const int col = 32 * ks + 8 * (lane >> 4);
+        fst8(dst + i * 8, r < rows ? fld8(W + (int64_t)(row0 + r) * K + col) : fzero8());
+    }
+}
+
+// ---- LayerNorm of a row tile into fragment-major LDS ---------------------------------------
+//
+// R rows of a row-major [M][K] fp16 matrix; 256 / R threads per row, each holding K / (8 TPR)
+// 16-byte chunks (chunk c = part + TPR j). QUAD picks the channel-major A-operand layout
+// (quad_row), otherwise the transposed product's B-operand layout.
+template <int K, int R>
+struct RowTile {
+    static constexpr int kTPR = kFThreads / R;
+    static constexpr int kChunks = K / 8 / kTPR;
+    half8 v[kChunks];
+};
+
+template <int K, int R>
+__device__ __forceinline__ void fetch_rows(RowTile<K, R>& t, const half_t* x, int M, int m0) {
+    constexpr int TPR = RowTile<K, R>::kTPR;
+    const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+#pragma unroll
+    for (int j = 0; j < RowTile<K, R>::kChunks; ++j) {
+        const int c = part + TPR * j;
+        t.v[j] = m0 + row < M ? fld8(x + (int64_t)(m0 + row) * K + 8 * c) : fzero8();
+    }
+}
+
+template <int TPR>
+__device__ __forceinline__ float group_sum(float s) {
+    if (TPR >= 2) s += __shfl_xor(s, 1);
+    if (TPR >= 4) s += __shfl_xor(s, 2);
+    if (TPR >= 8) s += __shfl_xor(s, 4);
+    return s;
+}
+
+template <int K, int R, bool QUAD, bool LN>
+__device__ __forceinline__ void ln_rows_to_frags(half_t* Xf, const RowTile<K, R>& t,
+                                                 const float* sc, const float* of, float eps) {
+    using RT = RowTile<K, R>;
+    constexpr int TPR = RT::kTPR, KS = K / 32;
+    const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+    float mean = 0.f, rstd = 1.f;
+    if constexpr (LN) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < RT::kChunks; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += (float)t.v[j][e];
+        mean = group_sum<TPR>(s) * (1.f / K);
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < RT::kChunks; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = (float)t.v[j][e] - mean;
+                q += d * d;
+            }
+        rstd = __builtin_amdgcn_rsqf(group_sum<TPR>(q) * (1.f / K) + eps);
+    }
+    int rb, rl;
+    if (QUAD) {
+        rb = (row >> 2) & 3;
+        rl = 4 * (row >> 4) + (row & 3);
+        rb += 4 * (row / 64);  // tiles taller than 64 rows stack 4-block groups
+        rl = 4 * ((row & 63) >> 4) + (row & 3);
+    } else {
+        rb = row >> 4;
+        rl = row & 15;
+    }
+#pragma unroll
+    for (int j = 0; j < RT::kChunks; ++j) {
+        const int c = part + TPR * j;
+        half8 y;
+        if constexpr (LN) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = 8 * c + e;
+                y[e] = (half_t)(((float)t.v[j][e] - mean) * rstd * sc[col] + of[col]);
+            }
+        } else {
+            y = t.v[j];
+        }
+        fst8(Xf + frag(rb, c >> 2, KS, rl + 16 * (c & 3)), y);
+    }
+}
+
+// ---- ln_projection / output_projection --------------------------------------------------
+
+struct ProjArgs {
+    const half_t* x;
+    const float* scale;
+    const float* offset;
+    const half_t* wT;        // [n][K]
+    const half_t* wbT;       // [heads][K]
+    const half_t* b;         // [n] or null
+    const half_t* residual;  // [M][n] or null (may alias out)
+    const half_t* keep;      // [M] or null
+    half_t* out;             // [M][n]
+    half_t* bias;            // [heads][M]
+    int M, n, heads;
+    int cols;                // columns per workgroup column chunk (multiple of 32)
+    float eps;
+};
+
+template <int K, bool LN>
+__global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
+    constexpr int KS = K / 32;
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    const int col0 = blockIdx.y * a.cols;
+    const int ncols = min(a.cols, a.n - col0);
+    const bool do_heads = blockIdx.y == 0 && a.heads > 0;
+    const int npairs = ncols > 0 ? ncols / 32 : 0;
+    half_t* Wf = lds;                                  // npairs * 2 blocks
+    half_t* Hf = Wf + npairs * 32 * K;                 // one block of head rows
+    half_t* Xf = Hf + (do_heads ? 16 * K : 0);         // 4 row blocks
+    float* sc = reinterpret_cast<float*>(Xf + kTileRows * K);
+    float* of = sc + K;
+
+    if (npairs > 0) load_weight_frags<K, true>(Wf, a.wT, ncols, 2 * npairs, col0);
+    if (do_heads) load_weight_frags<K, false>(Hf, a.wbT, a.heads, 1);
+    if constexpr (LN) {
+        for (int i = threadIdx.x; i < K; i += kFThreads) {
+            sc[i] = a.scale[i];
+            of[i] = a.offset[i];
+        }
+    }
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int head_wave = npairs % kFWaves;
+
+    RowTile<K, kTileRows> xt;
+    if (blockIdx.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, blockIdx.x * kTileRows);
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const int m0 = tile * kTileRows;
+        const int work = tile_work(a.keep, a.M, m0, kTileRows, -1.f);
+        if (work != kCompute) {
+            if (work == kPadding) {
+                // with a residual the output aliases it, which padding keeps
+                if (ncols > 0 && a.residual == nullptr) {
+                    for (int i = threadIdx.x; i < kTileRows * ncols / 8; i += kFThreads) {
+                        const int r = i / (ncols / 8), c = (i % (ncols / 8)) * 8;
+                        if (m0 + r < a.M) fst8(a.out + (int64_t)(m0 + r) * a.n + col0 + c, fzero8());
+                    }
+                }
+                if (do_heads) {
+                    for (int i = threadIdx.x; i < kTileRows * a.heads; i += kFThreads) {
+                        const int h = i / kTileRows, r = i % kTileRows;
+                        if (m0 + r < a.M) a.bias[(int64_t)h * a.M + m0 + r] = (half_t)0.f;
+                    }
+                }
+            }
+            if (tile + gridDim.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, (tile + gridDim.x) * kTileRows);
+            continue;
+        }
+        __syncthreads();  // the previous tile's operand reads are done
+        ln_rows_to_frags<K, kTileRows, false, LN>(Xf, xt, sc, of, a.eps);
+        __syncthreads();
+        if (tile + gridDim.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, (tile + gridDim.x) * kTileRows);
+
+        half8 xop[4][KS];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
+
+        for (int cp = wave; cp < npairs; cp += kFWaves) {
+            float4v acc[2][4];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const half8 w = fld8(Wf + frag(2 * cp + hb, ks, KS, lane));
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) acc[hb][rb] = mfma16x16x32(w, xop[rb][ks], acc[hb][rb]);
+                }
+            }
+            const int col = col0 + 32 * cp + 8 * g;
+            float bv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bv[j] = a.b ? (float)a.b[col + j] : 0.f;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int row = m0 + 16 * rb + r16;
+                if (row >= a.M) continue;
+                half_t* dst = a.out + (int64_t)row * a.n + col;
+                half8 res = a.residual ? fld8(a.residual + (int64_t)row * a.n + col) : fzero8();
+                half8 o;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[j] + (float)res[j]);
+                fst8(dst, o);
+            }
+        }
+        if (do_heads && wave == head_wave) {
+            float4v acc[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) acc[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 w = fld8(Hf + frag(0, ks, KS, lane));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma16x16x32(w, xop[rb][ks], acc[rb]);
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int row = m0 + 16 * rb + r16;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int h = 4 * g + i;
+                    if (h < a.heads && row < a.M) a.bias[(int64_t)h * a.M + row] = (half_t)acc[rb][i];
+                }
+            }
+        }
+    }
+}
+
+// ---- ln_gated_dual_proj ---------------------------------------------------------------------
+
+struct LnGdpArgs {
+    const half_t* x;
+    const float* scale;
+    const float* offset;
+    const half_t *wpT, *bp, *wgT, *bg, *mask;
+    half_t *left, *right;
+    int M, P;
+    float eps;
+};
+
+template <int K>
+__global__ __launch_bounds__(kFThreads) void ln_gdp_kernel(LnGdpArgs a) {
+    constexpr int KS = K / 32;
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    const int nb = a.P / 16;
+    half_t* Wp = lds;
+    half_t* Wg = Wp + a.P * K;
+    half_t* Xf = Wg + a.P * K;
+    float* sc = reinterpret_cast<float*>(Xf + kTileRows * K);
+    float* of = sc + K;
+    load_weight_frags<K, false>(Wp, a.wpT, a.P, nb);
+    load_weight_frags<K, false>(Wg, a.wgT, a.P, nb);
+    for (int i = threadIdx.x; i < K; i += kFThreads) {
+        sc[i] = a.scale[i];
+        of[i] = a.offset[i];
+    }
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int ci = a.P / 2;
+    const bool vec = (a.M & 7) == 0;
+
+    RowTile<K, kTileRows> xt;
+    if (blockIdx.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, blockIdx.x * kTileRows);
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const int m0 = tile * kTileRows;
+        // the mask is the keep: rows past M count as zero (volta_ops.cu:349)
+        const int work = tile_work(a.mask, a.M, m0, kTileRows, 0.f);
+        if (work != kCompute) {
+            if (work == kPadding) {
+                for (int i = threadIdx.x; i < kTileRows * ci; i += kFThreads) {
+                    const int c = i / kTileRows, r = i % kTileRows;
+                    if (m0 + r < a.M) {
+                        a.left[(int64_t)c * a.M + m0 + r] = (half_t)0.f;
+                        a.right[(int64_t)c * a.M + m0 + r] = (half_t)0.f;
+                    }
+                }
+            }
+            if (tile + gridDim.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, (tile + gridDim.x) * kTileRows);
+            continue;
+        }
+        __syncthreads();
+        ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
+        __syncthreads();
+        if (tile + gridDim.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, (tile + gridDim.x) * kTileRows);
+
+        half8 xop[4][KS];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
+        // lane group g holds rows m0 + 16 g .. +15: their mask, max(mask, 0), 0 past M
+        float mv[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int row = m0 + 16 * g + t;
+            mv[t] = row < a.M ? fmaxf((float)a.mask[row], 0.f) : 0.f;
+        }
+        for (int cb = wave; cb < nb; cb += kFWaves) {
+            float4v ap[4], ag[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                ap[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                ag[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 wp = fld8(Wp + frag(cb, ks, KS, lane));
+                const half8 wg = fld8(Wg + frag(cb, ks, KS, lane));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    ap[rb] = mfma16x16x32(xop[rb][ks], wp, ap[rb]);
+                    ag[rb] = mfma16x16x32(xop[rb][ks], wg, ag[rb]);
+                }
+            }
+            const int col = 16 * cb + r16;
+            const float bpv = (float)a.bp[col], bgv = (float)a.bg[col];
+            half_t* dst = (col < ci ? a.left + (int64_t)col * a.M : a.right + (int64_t)(col - ci) * a.M) +
+                          m0 + 16 * g;
+            half8 lo, hi;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 4 * rb + i;
+                    const float v = mv[t] * (ap[rb][i] + bpv) * sigmoid_fast(ag[rb][i] + bgv);
+                    if (t < 8) lo[t] = (half_t)v; else hi[t - 8] = (half_t)v;
+                }
+            const int rows_left = a.M - (m0 + 16 * g);
+            if (vec && rows_left >= 16) {
+                fst8(dst, lo);
+                fst8(dst + 8, hi);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 16; ++t)
+                    if (t < rows_left) dst[t] = t < 8 ? lo[t] : hi[t - 8];
+            }
+        }
+    }
+}
+
+// ---- trimul_epilogue --------------------------------------------------------------------------
+
+struct EpiArgs {
+    const float* x_cm;  // [C][M]
+    const half_t* x;    // [M][CA]
+    const float *in_scale, *in_offset, *ln_scale, *ln_offset;
+    const half_t *woT, *bo, *wgT, *bg;  // woT [O][C], wgT [O][CA]
+    const half_t* keep;
+    half_t* out;  // [M][O], may alias x with add_input
+    int M, O;
+    float eps;
+};
+
+template <int C, int CA, bool ADD>
+__global__ __launch_bounds__(kFThreads) void epilogue_kernel(EpiArgs a) {
+    constexpr int KC = C / 32, KA = CA / 32;
+    constexpr int kSub = 32;  // the reference's keep granularity here (volta_gdp.h:41)
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    const int nb = a.O / 16, npairs = a.O / 32;
+    half_t* Wo = lds;
+    half_t* Wg = Wo + a.O * C;
+    half_t* Yf = Wg + a.O * CA;
+    half_t* Af = Yf + kTileRows * C;
+    float* lsc = reinterpret_cast<float*>(Af + kTileRows * CA);
+    float* lof = lsc + C;
+    float* isc = lof + C;
+    float* iof = isc + CA;
+    float* red = iof + CA;  // [4][64]
+    load_weight_frags<C, true>(Wo, a.woT, a.O, nb);
+    load_weight_frags<CA, true>(Wg, a.wgT, a.O, nb);
+    for (int i = threadIdx.x; i < C; i += kFThreads) {
+        lsc[i] = a.ln_scale[i];
+        lof[i] = a.ln_offset[i];
+    }
+    for (int i = threadIdx.x; i < CA; i += kFThreads) {
+        isc[i] = a.in_scale[i];
+        iof[i] = a.in_offset[i];
+    }
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows;
+
+    RowTile<CA, kTileRows> xt;
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const int m0 = tile * kTileRows;
+        const int w0 = tile_work(a.keep, a.M, m0, kSub, -1.f);
+        const int w1 = tile_work(a.keep, a.M, m0 + kSub, kSub, -1.f);
+        if (w0 != kCompute && w1 != kCompute) {
+            if (!ADD) {  // with add_input the output aliases x, which padding keeps
+                for (int i = threadIdx.x; i < kTileRows * a.O / 8; i += kFThreads) {
+                    const int r = i / (a.O / 8), c = (i % (a.O / 8)) * 8;
+                    const int w = r < kSub ? w0 : w1;
+                    if (w == kPadding && m0 + r < a.M) fst8(a.out + (int64_t)(m0 + r) * a.O + c, fzero8());
+                }
+            }
+            continue;
+        }
+        fetch_rows<CA, kTileRows>(xt, a.x, a.M, m0);
+        // column LayerNorm of x_cm[:, m0 .. m0+63]: thread = (row r, channel quarter cq)
+        const int r = threadIdx.x % kTileRows, cq = threadIdx.x / kTileRows;
+        constexpr int CQ = C / 4;
+        float v[CQ];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < CQ; ++i) {
+            v[i] = m0 + r < a.M ? a.x_cm[(int64_t)(cq * CQ + i) * a.M + m0 + r] : 0.f;
+            s += v[i];
+        }
+        __syncthreads();  // the previous tile's operand and reduction reads are done
+        red[cq * kTileRows + r] = s;
+        __syncthreads();
+        const float mean = (red[r] + red[kTileRows + r] + red[2 * kTileRows + r] + red[3 * kTileRows + r]) * (1.f / C);
+        float q = 0.f;
+#pragma unroll
+        for (int i = 0; i < CQ; ++i) {
+            v[i] -= mean;
+            q += v[i] * v[i];
+        }
+        __syncthreads();
+        red[cq * kTileRows + r] = q;
+        __syncthreads();
+        const float var = (red[r] + red[kTileRows + r] + red[2 * kTileRows + r] + red[3 * kTileRows + r]) * (1.f / C);
+        const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
+#pragma unroll
+        for (int i = 0; i < CQ; i += 8) {
+            half8 y;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int c = cq * CQ + i + e;
+                y[e] = (half_t)(v[i + e] * rstd * lsc[c] + lof[c]);
+            }
+            const int c = (cq * CQ + i) / 8;
+            fst8(Yf + frag(r >> 4, c >> 2, KC, (r & 15) + 16 * (c & 3)), y);
+        }
+        ln_rows_to_frags<CA, kTileRows, false, true>(Af, xt, isc, iof, a.eps);
+        __syncthreads();
+
+        for (int cp = wave; cp < npairs; cp += kFWaves) {
+            float4v ao[2][4], ag[2][4];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    ao[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                    ag[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+            for (int ks = 0; ks < KC; ++ks) {
+                half8 yop[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) yop[rb] = fld8(Yf + frag(rb, ks, KC, lane));
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const half8 w = fld8(Wo + frag(2 * cp + hb, ks, KC, lane));
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) ao[hb][rb] = mfma16x16x32(w, yop[rb], ao[hb][rb]);
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < KA; ++ks) {
+                half8 aop[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) aop[rb] = fld8(Af + frag(rb, ks, KA, lane));
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const half8 w = fld8(Wg + frag(2 * cp + hb, ks, KA, lane));
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) ag[hb][rb] = mfma16x16x32(w, aop[rb], ag[hb][rb]);
+                }
+            }
+            const int col = 32 * cp + 8 * g;
+            float bov[8], bgv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                bov[j] = (float)a.bo[col + j];
+                bgv[j] = (float)a.bg[col + j];
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int lr = 16 * rb + r16, row = m0 + lr;
+                const int w = lr < kSub ? w0 : w1;
+                if (row >= a.M || w == kSkip || (ADD && w == kPadding)) continue;
+                half_t* dst = a.out + (int64_t)row * a.O + col;
+                if (w == kPadding) {
+                    fst8(dst, fzero8());
+                    continue;
+                }
+                half8 xa = ADD ? fld8(a.x + (int64_t)row * CA + col) : fzero8();
+                half8 o;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float val = (ao[j >> 2][rb][j & 3] + bov[j]) *
+                                      sigmoid_fast(ag[j >> 2][rb][j & 3] + bgv[j]);
+                    o[j] = (half_t)(val + (float)xa[j]);
+                }
+                fst8(dst, o);
+            }
+        }
+    }
+}
+
+// ---- transition -------------------------------------------------------------------------------
+//
+// out^T = W2^T relu(W1 X^T + b1) + b2 over hidden chunks of 64: the first product's accumulator
+// (rows = hidden units in pair order) is exactly the B operand of the second, so the hidden
+// activation never leaves registers. Weight chunks stream through LDS; a 128-row tile (32 rows a
+// wave) amortises each chunk over 64 MFMAs per wave.
+constexpr int kHid = 64;
+constexpr int kTransRows = 128;
+
+struct TransArgs {
+    const half_t* x;
+    const float *scale, *offset;
+    const half_t *w1T, *b1, *w2T, *b2;  // w1T [H][C], w2T [H/64][C][64]
+    const half_t* keep;
+    half_t* out;
+    int M, H;
+    float eps;
+};
+
+template <int C>
+struct TransTile {
+    static constexpr int KS = C / 32;
+    static constexpr int kW1 = 4 * KS * kWave * 8;        // halfs: 4 hidden blocks
+    static constexpr int kW2 = (C / 16) * 2 * kWave * 8;  // halfs: C/16 blocks x 2 steps
+    static constexpr int kChunks = (kW1 + kW2) / 8;
+    static constexpr int kCPT = kChunks / kFThreads;
+    static constexpr int kSub = C > 128 ? 32 : 64;        // keep granularity (volta_ops.cu:551-553)
+};
+
+template <int C, bool ADD>
+__global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
+    using T = TransTile<C>;
+    constexpr int KS = T::KS, NCB = C / 16, NSUB = kTransRows / T::kSub;
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    half_t* Xf = lds;                          // 8 row blocks
+    half_t* W1 = Xf + kTransRows * C;          // hidden chunk of w1, then of w2
+    half_t* W2 = W1 + T::kW1;
+    float* sc = reinterpret_cast<float*>(W2 + T::kW2);
+    float* of = sc + C;
+    for (int i = threadIdx.x; i < C; i += kFThreads) {
+        sc[i] = a.scale[i];
+        of[i] = a.offset[i];
+    }
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTransRows - 1) / kTransRows;
+    const int chunks = a.H / kHid;
+
+    // weight chunk j: W1 fragments of hidden rows 64 j + pair_row(hb, r), W2 fragments of output
+    // channels pair_row(cb, r) over hidden 64 j + 32 kt + 8 g ..
+    half8 wreg[T::kCPT];
+    const auto fetch_w = [&](int j) {
+#pragma unroll
+        for (int u = 0; u < T::kCPT; ++u) {
+            const int i = threadIdx.x + u * kFThreads;
+            const int l = i % kWave, t = i / kWave;
+            if (i < T::kW1 / 8) {
+                const int ks = t % KS, hb = t / KS;
+                const int hid = kHid * j + pair_row(hb, l & 15);
+                wreg[u] = fld8(a.w1T + (int64_t)hid * C + 32 * ks + 8 * (l >> 4));
+            } else {
+                const int t2 = t - T::kW1 / (8 * kWave);
+                const int kt = t2 & 1, cb = t2 >> 1;
+                const int c = pair_row(cb, l & 15);
+                wreg[u] = fld8(a.w2T + ((int64_t)j * C + c) * kHid + 32 * kt + 8 * (l >> 4));
+            }
+        }
+    };
+    const auto store_w = [&]() {
+#pragma unroll
+        for (int u = 0; u < T::kCPT; ++u) fst8(W1 + (threadIdx.x + u * kFThreads) * 8, wreg[u]);
+    };
+
+    RowTile<C, kTransRows> xt;
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+        const int m0 = tile * kTransRows;
+        int work[NSUB];
+        bool any = false;
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            work[s] = tile_work(a.keep, a.M, m0 + s * T::kSub, T::kSub, -1.f);
+            any |= work[s] == kCompute;
+        }
+        if (!any) {
+            if (!ADD) {
+                for (int i = threadIdx.x; i < kTransRows * C / 8; i += kFThreads) {
+                    const int r = i / (C / 8), c = (i % (C / 8)) * 8;
+                    if (work[r / T::kSub] == kPadding && m0 + r < a.M)
+                        fst8(a.out + (int64_t)(m0 + r) * C + c, fzero8());
+                }
+            }
+            continue;
+        }
+        fetch_rows<C, kTransRows>(xt, a.x, a.M, m0);
+        fetch_w(0);
+        __syncthreads();
+        ln_rows_to_frags<C, kTransRows, false, true>(Xf, xt, sc, of, a.eps);
+
+        float4v acc[NCB][2];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) acc[cb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+        half8 xop[2][KS];
+        for (int j = 0; j < chunks; ++j) {
+            __syncthreads();  // the previous chunk's weight reads are done
+            store_w();
+            __syncthreads();
+            if (j == 0) {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(2 * wave + rb, ks, KS, lane));
+            }
+            if (j + 1 < chunks) fetch_w(j + 1);
+
+            // hidden^T for 64 units x this wave's 32 rows
+            float4v hacc[4][2];
+#pragma unroll
+            for (int hb = 0; hb < 4; ++hb)
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb) hacc[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int hb = 0; hb < 4; ++hb) {
+                    const half8 w = fld8(W1 + frag(hb, ks, KS, lane));
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb) hacc[hb][rb] = mfma16x16x32(w, xop[rb][ks], hacc[hb][rb]);
+                }
+            }
+            // relu(. + b1), fp16: slot 8 g + e of step kt is hidden unit 32 kt + 8 g + e
+            half8 hop[2][2];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                float b1v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) b1v[e] = (float)a.b1[kHid * j + 32 * kt + 8 * g + e];
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        hop[kt][rb][e] = (half_t)fmaxf(hacc[2 * kt + (e >> 2)][rb][e & 3] + b1v[e], 0.f);
+            }
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt) {
+                    const half8 w = fld8(W2 + frag(cb, kt, 2, lane));
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb) acc[cb][rb] = mfma16x16x32(w, hop[kt][rb], acc[cb][rb]);
+                }
+            }
+        }
+
+        // lane: channels 32 (cb/2) + 8 g .. +7 of rows m0 + 32 wave + 16 rb + r16
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const int lr = 32 * wave + 16 * rb + r16, row = m0 + lr;
+            const int w = work[lr / T::kSub];
+            if (row >= a.M || w == kSkip || (ADD && w == kPadding)) continue;
+#pragma unroll
+            for (int cp = 0; cp < NCB / 2; ++cp) {
+                const int col = 32 * cp + 8 * g;
+                half_t* dst = a.out + (int64_t)row * C + col;
+                if (w == kPadding) {
+                    fst8(dst, fzero8());
+                    continue;
+                }
+                const half8 xa = ADD ? fld8(a.x + (int64_t)row * C + col) : fzero8();
+                half8 o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    o[e] = (half_t)(acc[2 * cp + (e >> 2)][rb][e & 3] + (float)a.b2[col + e] + (float)xa[e]);
+                fst8(dst, o);
+            }
+        }
+    }
+}
+
+// ---- host side --------------------------------------------------------------------------------
+
+static int fused_cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) {
+            cus = v;
+        } else {
+            cus = 256;
+        }
+    }
+    return cus;
+}
+
+static int fused_lds_limit() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    return shared_limit(dev);
+}
+
+template <typename F>
+static int launch_fused(const char* what, F kernel, dim3 grid, size_t lds, hipStream_t s,
+                        const void* args_ptr, size_t) {
+    (void)args_ptr;
+    const int limit = fused_lds_limit();
+    if (limit > 0 && lds > (size_t)limit) {
+        return invalid(std::string(what) + ": needs " + std::to_string(lds / 1024) +
+                       " KB shared, device allows " + std::to_string(limit / 1024) + " KB");
+    }
+    if (lds > 64 * 1024) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    }
+    (void)grid;
+    (void)s;
+    return CLK_OK;
+}
+
+static bool fused_width(int64_t c) { return c == 64 || c == 128; }
+static bool msa_width(int64_t c) { return fused_width(c) || c == 256; }
+
+static unsigned persistent_grid(int64_t tiles, size_t lds) {
+    const int limit = fused_lds_limit();
+    int per_cu = 2;
+    if (limit > 0 && lds > 0) per_cu = std::max(1, std::min(4, (int)(limit / lds)));
+    const int64_t g = std::min<int64_t>(tiles, (int64_t)fused_cu_count() * per_cu);
+    return (unsigned)std::max<int64_t>(g, 1);
+}
+
+}  // namespace clk
+
+using namespace clk;
+
+static const half_t* f16p(const clk_buffer* b) { return static_cast<const half_t*>(b->data); }
+static const float* f32p(const clk_buffer* b) { return static_cast<const float*>(b->data); }
+
+extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
+                          const clk_buffer* offset, const clk_buffer* wpT, const clk_buffer* bp,
+                          const clk_buffer* wgT, const clk_buffer* bg, const clk_buffer* mask,
+                          const clk_buffer* left, const clk_buffer* right, float eps) {
+    const clk_buffer* bufs[] = {x, scale, offset, wpT, bp, wgT, bg, mask, left, right};
+    const int types[] = {CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    if (int st = check_types("ln_gdp", bufs, types, 10)) return st;
+    if (x->rank != 2 || wpT->rank != 2 || wpT->dims[1] != x->dims[1]) {
+        return invalid("ln_gdp: x must be [M,K] and wpT [P,K]");
+    }
+    const int64_t M = x->dims[0], K = x->dims[1], P = wpT->dims[0];
+    if (!fused_width(K) || P % 2 || !fused_width(P / 2)) return invalid("ln_gdp: K and P/2 must be 64 or 128");
+    if (elements(wgT) != P * K || elements(bp) != P || elements(bg) != P || elements(mask) != M ||
+        elements(left) != P / 2 * M || elements(right) != P / 2 * M || elements(scale) != K ||
+        elements(offset) != K) {
+        return invalid("ln_gdp: shapes do not match x [M,K], wpT [P,K]");
+    }
+    if (M == 0) return ok();
+    if (!aligned16(x->data) || !aligned16(wpT->data) || !aligned16(wgT->data) || !aligned16(left->data) ||
+        !aligned16(right->data) || !aligned16(mask->data)) {
+        return invalid("ln_gdp: x, weights, mask and results must be 16-byte aligned");
+    }
+    LnGdpArgs a{f16p(x), f32p(scale), f32p(offset), f16p(wpT), f16p(bp), f16p(wgT), f16p(bg), f16p(mask),
+                static_cast<half_t*>(left->data), static_cast<half_t*>(right->data), (int)M, (int)P, eps};
+    const size_t lds = (size_t)(2 * P * K + kTileRows * K) * 2 + 2 * K * 4;
+    const int64_t tiles = (M + kTileRows - 1) / kTileRows;
+    const dim3 grid(persistent_grid(tiles, lds));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (K == 64) {
+        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64>, grid, lds, s, &a, 0)) return st;
+        hipLaunchKernelGGL(ln_gdp_kernel<64>, grid, dim3(kFThreads), lds, s, a);
+    } else {
+        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<128>, grid, lds, s, &a, 0)) return st;
+        hipLaunchKernelGGL(ln_gdp_kernel<128>, grid, dim3(kFThreads), lds, s, a);
+    }
+    return launch_status("ln_gdp");
+}
+
+template <int C, int CA, bool ADD>
+static int run_epilogue(const EpiArgs& a, hipStream_t s) {
+    const size_t lds = (size_t)(a.O * C + a.O * CA + kTileRows * C + kTileRows * CA) * 2 +
+                       (size_t)(2 * C + 2 * CA + 4 * kTileRows) * 4;
+    const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
+    const dim3 grid(persistent_grid(tiles, lds));
+    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, ADD>, grid, lds, s, &a, 0)) return st;
+    hipLaunchKernelGGL((epilogue_kernel<C, CA, ADD>), grid, dim3(kFThreads), lds, s, a);
+    return launch_status("trimul_epilogue");
+}
+
+template <int C>
+static int epilogue_dispatch(const EpiArgs& a, int64_t CA, bool add, hipStream_t s) {
+    if (CA == 64) return add ? run_epilogue<C, 64, true>(a, s) : run_epilogue<C, 64, false>(a, s);
+    return add ? run_epilogue<C, 128, true>(a, s) : run_epilogue<C, 128, false>(a, s);
+}
+
+extern "C" int clk_trimul_epilogue(clk_stream stream, const clk_buffer* x_cm, const clk_buffer* x,
+                                   const clk_buffer* in_scale, const clk_buffer* in_offset,
+                                   const clk_buffer* ln_scale, const clk_buffer* ln_offset,
+                                   const clk_buffer* woT, const clk_buffer* bo, const clk_buffer* wgT,
+                                   const clk_buffer* bg, const clk_buffer* keep, const clk_buffer* out,
+                                   float eps, int32_t add_input, int32_t has_keep) {
+    const clk_buffer* bufs[] = {x_cm, x, in_scale, in_offset, ln_scale, ln_offset, woT, bo, wgT, bg, keep, out};
+    const int types[] = {CLK_F32, CLK_F16, CLK_F32, CLK_F32, CLK_F32, CLK_F32,
+                         CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    if (int st = check_types("trimul_epilogue", bufs, types, 12)) return st;
+    if (x_cm->rank != 2 || x->rank != 2 || woT->rank != 2 || x->dims[0] != x_cm->dims[1] ||
+        woT->dims[1] != x_cm->dims[0]) {
+        return invalid("trimul_epilogue: x_cm [C,M], x [M,CA], woT [O,C]");
+    }
+    const int64_t C = x_cm->dims[0], M = x_cm->dims[1], CA = x->dims[1], O = woT->dims[0];
+    if (!fused_width(C) || !fused_width(CA) || !fused_width(O) || (add_input && O != CA)) {
+        return invalid("trimul_epilogue: C, CA and O must be 64 or 128, O == CA with add_input");
+    }
+    if (elements(wgT) != O * CA || elements(bo) != O || elements(bg) != O || elements(in_scale) != CA ||
+        elements(in_offset) != CA || elements(ln_scale) != C || elements(ln_offset) != C ||
+        elements(out) != M * O || (has_keep && elements(keep) != M)) {
+        return invalid("trimul_epilogue: shapes do not match");
+    }
+    if (M == 0) return ok();
+    if (!aligned16(x->data) || !aligned16(woT->data) || !aligned16(wgT->data) || !aligned16(out->data)) {
+        return invalid("trimul_epilogue: x, weights and out must be 16-byte aligned");
+    }
+    EpiArgs a{f32p(x_cm), f16p(x), f32p(in_scale), f32p(in_offset), f32p(ln_scale), f32p(ln_offset),
+              f16p(woT), f16p(bo), f16p(wgT), f16p(bg), has_keep ? f16p(keep) : nullptr,
+              static_cast<half_t*>(out->data), (int)M, (int)O, eps};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return C == 64 ? epilogue_dispatch<64>(a, CA, add_input, s) : epilogue_dispatch<128>(a, CA, add_input, s);
+}
+
+template <int K, bool LN>
+static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
+    ProjArgs a = a0;
+    // columns per workgroup: all of them while the weights fit beside the tile in LDS
+    const int limit = fused_lds_limit();
+    const size_t fixed = (size_t)(16 * K + kTileRows * K) * 2 + 2 * K * 4;
+    int cols = a.n;
+    if (limit > 0) {
+        while (cols > 32 && fixed + (size_t)cols * K * 2 > (size_t)limit) cols = (cols / 2 + 31) / 32 * 32;
+    }
+    a.cols = std::max(cols, 32);
+    const int chunks = a.n > 0 ? (a.n + a.cols - 1) / a.cols : 1;
+    const size_t lds = (size_t)(std::min(a.cols, std::max(a.n, 0)) * K) * 2 + fixed;
+    const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
+    const dim3 grid(persistent_grid(tiles, lds), chunks);
+    if (int st = launch_fused(what, proj_kernel<K, LN>, grid, lds, s, &a, 0)) return st;
+    hipLaunchKernelGGL((proj_kernel<K, LN>), grid, dim3(kFThreads), lds, s, a);
+    return launch_status(what);
+}
+
+extern "C" int clk_ln_projection(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
+                                 const clk_buffer* offset, const clk_buffer* wT, const clk_buffer* wbT,
+                                 const clk_buffer* keep, const clk_buffer* p, const clk_buffer* bias,
+                                 float eps, int64_t n, int64_t heads, int32_t has_keep) {
+    const clk_buffer* bufs[] = {x, scale, offset, wT, wbT, keep, p, bias};
+    const int types[] = {CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    if (int st = check_types("ln_projection", bufs, types, 8)) return st;
+    if (x->rank != 2) return invalid("ln_projection: x must be [M,K]");
+    const int64_t M = x->dims[0], K = x->dims[1];
+    if (!fused_width(K) || n < 0 || n % 64 || heads < 0 || heads > 8) {
+        return invalid("ln_projection: K must be 64 or 128, n a multiple of 64, at most 8 heads");
+    }
+    if (elements(scale) != K || elements(offset) != K ||
+        (n && (elements(wT) != n * K || elements(p) != M * n)) ||
+        (heads && (elements(wbT) != heads * K || elements(bias) != heads * M)) ||
+        (has_keep && elements(keep) != M)) {
+        return invalid("ln_projection: shapes do not match");
+    }
+    if (M == 0) return ok();
+    if (!aligned16(x->data) || (n && (!aligned16(wT->data) || !aligned16(p->data))) ||
+        (heads && !aligned16(wbT->data))) {
+        return invalid("ln_projection: x, weights and p must be 16-byte aligned");
+    }
+    if (n == 0 && heads == 0) return ok();
+    ProjArgs a{};
+    a.x = f16p(x);
+    a.scale = f32p(scale);
+    a.offset = f32p(offset);
+    a.wT = n ? f16p(wT) : nullptr;
+    a.wbT = heads ? f16p(wbT) : nullptr;
+    a.keep = has_keep ? f16p(keep) : nullptr;
+    a.out = n ? static_cast<half_t*>(p->data) : nullptr;
+    a.bias = heads ? static_cast<half_t*>(bias->data) : nullptr;
+    a.M = (int)M;
+    a.n = (int)n;
+    a.heads = (int)heads;
+    a.eps = eps;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return K == 64 ? run_proj<64, true>(a, s, "ln_projection") : run_proj<128, true>(a, s, "ln_projection");
+}
+
+extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, const clk_buffer* wT,
+                                     const clk_buffer* b, const clk_buffer* residual,
+                                     const clk_buffer* keep, const clk_buffer* out, int32_t has_residual,
+                                     int32_t has_keep) {
+    const clk_buffer* bufs[] = {o, wT, b, residual, keep, out};
+    const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    if (int st = check_types("output_projection", bufs, types, 6)) return st;
+    if (o->rank != 2 || wT->rank != 2 || wT->dims[1] != o->dims[1]) {
+        return invalid("output_projection: o must be [M,K] and wT [N,K]");
+    }
+    const int64_t M = o->dims[0], K = o->dims[1], N = wT->dims[0];
+    if (!fused_width(K) || !fused_width(N)) return invalid("output_projection: K and N must be 64 or 128");
+    if (elements(b) != N || elements(out) != M * N || (has_residual && elements(residual) != M * N) ||
+        (has_keep && elements(keep) != M)) {
+        return invalid("output_projection: shapes do not match");
+    }
+    if (M == 0) return ok();
+    if (!aligned16(o->data) || !aligned16(wT->data) || !aligned16(out->data) ||
+        (has_residual && !aligned16(residual->data))) {
+        return invalid("output_projection: o, wT, residual and out must be 16-byte aligned");
+    }
+    ProjArgs a{};
+    a.x = f16p(o);
+    a.wT = f16p(wT);
+    a.b = f16p(b);
+    a.residual = has_residual ? f16p(residual) : nullptr;
+    a.keep = has_keep ? f16p(keep) : nullptr;
+    a.out = static_cast<half_t*>(out->data);
+    a.M = (int)M;
+    a.n = (int)N;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return K == 64 ? run_proj<64, false>(a, s, "output_projection") : run_proj<128, false>(a, s, "output_projection");
+}
+
+template <int C, bool ADD>
+static int run_transition(const TransArgs& a, hipStream_t s) {
+    using T = TransTile<C>;
+    const size_t lds = (size_t)(kTransRows * C + T::kW1 + T::kW2) * 2 + 2 * C * 4;
+    const int64_t tiles = (a.M + kTransRows - 1) / kTransRows;
+    const dim3 grid(persistent_grid(tiles, lds));
+    if (int st = launch_fused("transition", transition_kernel<C, ADD>, grid, lds, s, &a, 0)) return st;
+    hipLaunchKernelGGL((transition_kernel<C, ADD>), grid, dim3(kFThreads), lds, s, a);
+    return launch_status("transition");
+}
+
+extern "C" int clk_transition(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
+                              const clk_buffer* offset, const clk_buffer* w1T, const clk_buffer* b1,
+                              const clk_buffer* w2T, const clk_buffer* b2, const clk_buffer* keep,
+                              const clk_buffer* out, float eps, int32_t add_input, int32_t has_keep) {
+    const clk_buffer* bufs[] = {x, scale, offset, w1T, b1, w2T, b2, keep, out};
+    const int types[] = {CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    if (int st = check_types("transition", bufs, types, 9)) return st;
+    if (x->rank != 2 || w1T->rank != 2 || w1T->dims[1] != x->dims[1]) {
+        return invalid("transition: x must be [M,C] and w1T [H,C]");
+    }
+    const int64_t M = x->dims[0], C = x->dims[1], H = w1T->dims[0];
+    if (!msa_width(C) || (H != 2 * C && H != 4 * C)) {
+        return invalid("transition: C must be 64, 128 or 256, H 2C or 4C");
+    }
+    if (elements(scale) != C || elements(offset) != C || elements(b1) != H || elements(w2T) != H * C ||
+        elements(b2) != C || elements(out) != M * C || (has_keep && elements(keep) != M)) {
+        return invalid("transition: shapes do not match");
+    }
+    if (M == 0) return ok();
+    if (!aligned16(x->data) || !aligned16(w1T->data) || !aligned16(w2T->data) || !aligned16(out->data)) {
+        return invalid("transition: x, weights and out must be 16-byte aligned");
+    }
+    TransArgs a{f16p(x), f32p(scale), f32p(offset), f16p(w1T), f16p(b1), f16p(w2T), f16p(b2),
+                has_keep ? f16p(keep) : nullptr, static_cast<half_t*>(out->data), (int)M, (int)H, eps};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (C == 64) return add_input ? run_transition<64, true>(a, s) : run_transition<64, false>(a, s);
+    if (C == 128) return add_input ? run_transition<128, true>(a, s) : run_transition<128, false>(a, s);
+    return add_input ? run_transition<256, true>(a, s) : run_transition<256, false>(a, s);
+}

@@ -1,0 +1,63 @@
+"""pytest setup: the `gpu` marker, import paths and shared helpers for the parity tests."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "colabfold-legacy-kernels_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built library")
+
+
+def gpu_available():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:  # noqa: BLE001
+        return False
+
+
+@pytest.fixture(scope="session")
+def hip():
+    """The gfx950 front end; a GPU test without a GPU or without the library fails loudly."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("gpu test on a machine without a GPU")
+    from colabfold_legacy_kernels import hip as h
+    h.lib()
+    return h
+
+
+def ulp16(x):
+    """One fp16 ulp at |x| (subnormal spacing below 2^-14)."""
+    a = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def rel(a, b):
+    """The reference tests' error metric (tests/test_attn_bwd.py:104-111)."""
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    if not np.isfinite(a).all():
+        return float("inf")
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-3)) if a.size else 0.0
+
+
+def abs_excess(got, want, fp16_out=True):
+    """max |got - want| beyond half an fp16 ulp of want (the unavoidable output rounding)."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    if got.size == 0:
+        return 0.0
+    if not np.isfinite(got).all():
+        return float("inf")
+    err = np.abs(got - want)
+    if fp16_out:
+        err = err - 0.5 * ulp16(want)
+    return float(max(err.max(), 0.0))

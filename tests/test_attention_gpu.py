@@ -1,0 +1,155 @@
+"""VoltaMma / VoltaMmaBwd on gfx950 against the float64 oracle, through the C ABI.
+
+The cases follow the reference's tests/test_attn_bwd.py (base shapes 379-385, all-masked rows
+175-181, every forward (D, block_q, block_k) 184-204, large amplitudes 207-221, tiny shapes
+224-237, repeat determinism 240-259, the grid-order threshold 330-341, want flags 344-369),
+with inputs drawn as its inputs() does (114-125).
+
+Tolerances (fp16 I/O): the reference's relative metric rel < 0.05 everywhere, and at unit-scale
+amplitudes an absolute bar beyond the half-ulp rounding of each fp16 result: outputs (out, lse)
+<= 2e-3, gradients (dq, dk, dv, dbias) <= 5e-3. dq, dk, dv and dbias must also repeat
+bit-for-bit (the backward has no atomics), which is stronger than the reference's bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import abs_excess, rel
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+OUT_ATOL = 2e-3
+GRAD_ATOL = 5e-3
+REL_TOL = 0.05
+
+FWD_CONFIGS = ((8, 64, 64), (8, 64, 32), (8, 32, 32), (8, 128, 64), (8, 32, 64),
+               (32, 64, 64), (32, 64, 32), (32, 32, 64), (32, 32, 32), (32, 128, 64),
+               (32, 16, 64), (16, 64, 64), (16, 32, 32), (16, 64, 32), (64, 64, 64),
+               (64, 32, 32), (24, 64, 32), (24, 32, 32), (48, 64, 32), (48, 32, 32),
+               (96, 64, 32), (96, 32, 32))
+
+
+def inputs(n, h, sq, sk, d, seed, masked_rows=0.15, qk_amp=0.5, vo_amp=0.5):
+    rng = np.random.default_rng(seed)
+    f16 = lambda x: np.asarray(x, np.float16)
+    q = f16(rng.standard_normal((n, h, sq, d)) * qk_amp)
+    k = f16(rng.standard_normal((n, h, sk, d)) * qk_amp)
+    v = f16(rng.standard_normal((n, h, sk, d)) * vo_amp)
+    bias = f16(rng.standard_normal((h, sq, sk)) * qk_amp)
+    kmask = (rng.random((n, sk)) > masked_rows).astype(np.uint8)
+    dout = f16(rng.standard_normal((n, h, sq, d)) * vo_amp)
+    return q, k, v, bias, kmask, dout
+
+
+def dev(*xs):
+    return [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in xs]
+
+
+def host(*ts):
+    torch.cuda.synchronize()
+    return [t.float().cpu().numpy() for t in ts]
+
+
+def run(hip, n=3, h=4, sq=96, sk=96, d=32, seed=0, bq=64, bk=32, kmask=None, qk_amp=0.5,
+        vo_amp=0.5, want_lse=True, want_dbias=True):
+    q, k, v, bias, km, dout = inputs(n, h, sq, sk, d, seed, qk_amp=qk_amp, vo_amp=vo_amp)
+    if kmask is not None:
+        km = kmask
+    scale = float(d) ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale, bq, bk, want_lse=True)
+    dq, dk, dv, dbias = hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale,
+                                          want_dbias=want_dbias)
+    got = dict(zip(("out", "lse", "dq", "dk", "dv", "dbias"), host(out, lse, dq, dk, dv, dbias)))
+    ref_out, ref_lse = ora.attention_fwd(q, k, v, bias, km, scale)
+    ref = dict(zip(("dq", "dk", "dv", "dbias"), ora.attention_bwd(q, k, v, bias, km, dout, scale)))
+    ref["out"], ref["lse"] = ref_out, ref_lse
+    return got, ref
+
+
+def check(got, ref, label, absolute=True):
+    bad = []
+    for name in ("out", "lse", "dq", "dk", "dv", "dbias"):
+        r = rel(got[name], ref[name])
+        msg = "%s %s rel %.2e" % (label, name, r)
+        if r >= REL_TOL:
+            bad.append(msg)
+        if absolute:
+            tol = OUT_ATOL if name in ("out", "lse") else GRAD_ATOL
+            e = abs_excess(got[name], ref[name], fp16_out=name not in ("lse", "dbias"))
+            if e > tol:
+                bad.append("%s %s abs excess %.2e > %.0e" % (label, name, e, tol))
+    assert not bad, "; ".join(bad)
+
+
+@pytest.mark.parametrize("kw", [dict(sq=96, sk=96, d=32), dict(sq=96, sk=96, d=32, bq=64, bk=64),
+                                dict(sq=64, sk=64, d=64, bk=64), dict(sq=70, sk=83, d=16),
+                                dict(sq=128, sk=32, d=8, n=1, h=1)])
+def test_base_shapes(hip, kw):
+    got, ref = run(hip, **kw)
+    check(got, ref, str(kw))
+
+
+def test_all_masked_row(hip):
+    """A batch element with every key masked: a uniform softmax, finite lse, zero dS."""
+    km = np.ones((3, 96), np.uint8)
+    km[1, :] = 0
+    got, ref = run(hip, kmask=km)
+    check(got, ref, "all-masked")
+    # the closed form: out = mean of v, lse2 = log2(Sk) - 1e4 log2(e)
+    lse_row = got["lse"][1]
+    assert np.allclose(lse_row, np.log2(96) + ora.MASKED_LOGIT * ora.LOG2E, atol=2e-3)
+
+
+@pytest.mark.parametrize("d,bq,bk", FWD_CONFIGS)
+def test_every_forward_config(hip, d, bq, bk):
+    got, ref = run(hip, n=2, h=2, sq=130, sk=130, d=d, bq=bq, bk=bk)
+    check(got, ref, "D=%d bq=%d bk=%d" % (d, bq, bk))
+
+
+@pytest.mark.parametrize("qk,vo", [(0.5, 32.0), (0.5, 90.0), (16.0, 0.5), (32.0, 0.5)])
+def test_large_amplitudes(hip, qk, vo):
+    got, ref = run(hip, n=2, h=2, d=64, bk=64, qk_amp=qk, vo_amp=vo)
+    check(got, ref, "qk x%g vo x%g" % (qk, vo), absolute=False)
+
+
+@pytest.mark.parametrize("sq,sk,d", [(1, 1, 16), (1, 4, 16), (7, 13, 16), (33, 1, 32), (3, 96, 8)])
+def test_tiny_shapes(hip, sq, sk, d):
+    got, ref = run(hip, n=2, h=2, sq=sq, sk=sk, d=d)
+    check(got, ref, "sq=%d sk=%d d=%d" % (sq, sk, d))
+
+
+@pytest.mark.parametrize("n", [63, 64, 96])
+def test_batch_sizes(hip, n):
+    got, ref = run(hip, n=n, h=2, sq=64, sk=64, d=32)
+    check(got, ref, "n=%d" % n)
+
+
+def test_repeat_bit_exact(hip):
+    q, k, v, bias, km, dout = inputs(3, 4, 96, 96, 32, 0)
+    scale = 32.0 ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale)
+    a = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    b = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    for name, x, y in zip(("dq", "dk", "dv", "dbias"), a, b):
+        assert np.array_equal(x, y), name + " differs between identical calls"
+
+
+def test_want_flags(hip):
+    """want_lse and want_dbias only drop results (tests/test_attn_bwd.py:344-369)."""
+    q, k, v, bias, km, dout = inputs(2, 2, 96, 96, 32, 0)
+    scale = 32.0 ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale)
+    lse_one = torch.full((1,), 7.0, dtype=torch.float32, device="cuda")
+    out_off, lse_off = hip.attention_fwd(tq, tk, tv, tb, tm, scale, want_lse=False, lse=lse_one)
+    on = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    off = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale, want_dbias=False))
+    o1, o2, l1 = host(out, out_off, lse_off)
+    assert np.array_equal(o1, o2), "out changed when want_lse was off"
+    assert l1[0] == 7.0, "the one-element lse was written without want_lse"
+    for name, x, y in zip(("dq", "dk", "dv"), on[:3], off[:3]):
+        assert np.array_equal(x, y), name + " changed when want_dbias was off"
+    assert np.abs(off[3]).max() == 0.0, "dbias was written although want_dbias was off"

@@ -1,0 +1,117 @@
+"""VoltaMmaPacked / VoltaMmaPackedTrim on gfx950 against the float64 oracle.
+
+Cases are the reference's tests/test_packed_attention.py:88-93 (X, Y, H, D, column, masked
+fraction, live length): rows and columns, D from 8 to 64, lengths that are and are not
+multiples of 8, and live < S (trim). Inputs as its one() (60-71): p ~ N(0,1), bias ~ N(0,1),
+gate_bias ~ 0.1 N(0,1), a padded tail and a dead last row when live < S.
+
+Checks (fp16 I/O): every batch row against the oracle, which shares the kernels' -1e4 mask
+convention, with abs error beyond fp16 half-ulp rounding <= 2e-3 and the reference's 0.03 bar;
+with trim (test_packed_attention.py:76-85): live queries as the oracle, padded queries of a
+live row either the no-trim value or exactly zero, rows with no live key exactly zero. Large
+cases compare a subset of batch rows (the oracle's per-row math is independent across rows).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import abs_excess
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+OUT_ATOL = 2e-3
+
+CASES = ((384, 384, 4, 32, False, 0.01, 384), (96, 384, 8, 32, True, 0.01, 96),
+         (64, 256, 8, 8, False, 0.05, 256), (256, 64, 8, 8, True, 0.05, 64),
+         (16, 128, 4, 16, False, 0.3, 128), (12, 200, 4, 64, False, 0.01, 200),
+         (1, 261, 8, 32, True, 0.0, 1), (261, 1, 8, 32, False, 0.0, 1),
+         (3, 37, 4, 32, True, 0.2, 3), (4, 264, 4, 32, False, 0.05, 264),
+         (5, 129, 4, 32, True, 0.5, 5), (6, 256, 4, 32, False, 0.05, 200),
+         (256, 6, 4, 32, True, 0.05, 200), (4, 128, 8, 8, False, 0.05, 72),
+         (4, 261, 4, 32, False, 0.05, 200))
+
+
+def make(X, Y, H, D, column, frac, live, G=4):
+    rng = np.random.default_rng(0)
+    p = rng.normal(size=(X, Y, 4, H, D)).astype(np.float16)
+    if G == 3:
+        p = np.ascontiguousarray(p[:, :, :3])
+    N, S = (Y, X) if column else (X, Y)
+    bias = rng.normal(size=(H, S, S)).astype(np.float16)
+    gb = (rng.normal(size=(H, D)) * .1).astype(np.float16)
+    km = rng.random((N, S)) >= frac
+    if live < S:
+        km[:, live:] = False
+        km[-1] = False
+    return p, bias, gb, km.astype(np.uint8)
+
+
+def sample_rows(N, limit=24):
+    if N <= limit:
+        return np.arange(N)
+    return np.unique(np.concatenate([np.arange(8), np.arange(N - 8, N),
+                                     np.random.default_rng(1).choice(N, limit - 16, replace=False)]))
+
+
+def oracle_rows(p, bias, km, gb, column, rows, lims=None):
+    """The oracle on batch rows `rows` only, as [len(rows), S, H, D] (batch-major)."""
+    pb = np.transpose(p, (1, 0, 2, 3, 4)) if column else p
+    sub = pb[rows]
+    lm = None
+    if lims is not None:
+        lm = np.concatenate([lims[rows], lims[-1:]])
+    o = ora.attention_packed(sub, bias, km[rows], gb, False, lims=lm)
+    return o
+
+
+def to_batch_major(o, column):
+    o = o.float().cpu().numpy()
+    return np.transpose(o, (1, 0, 2, 3)) if column else o
+
+
+@pytest.mark.parametrize("case", CASES, ids=[str(c) for c in CASES])
+def test_packed(hip, case):
+    X, Y, H, D, column, frac, live = case
+    p, bias, gb, km = make(*case)
+    N, S = (Y, X) if column else (X, Y)
+    scale = D ** -0.5
+    bk = 64 if D == 64 else 32
+    tp, tb, tg, tk = (torch.from_numpy(a).cuda() for a in (p, bias, gb, km))
+    out = hip.attention_packed(tp, tb, tk, tg, scale, 64, bk, column)
+    o = to_batch_major(out, column)
+    rows = sample_rows(N)
+    ref = oracle_rows(p, bias, km, gb, column, rows)
+    e = abs_excess(o[rows], ref)
+    assert e <= OUT_ATOL, "max abs error beyond rounding %.2e" % e
+    assert np.abs(o[rows] - ref).max() < 0.03
+    if live >= S:
+        return
+    lims = ora.trim_limits(km)
+    tl = torch.from_numpy(lims).cuda()
+    t = to_batch_major(hip.attention_packed(tp, tb, tk, tg, scale, 64, bk, column, lims=tl), column)
+    alive = km.any(axis=1)
+    r_live = rows[alive[rows]]
+    if r_live.size:
+        ref_live = oracle_rows(p, bias, km, gb, column, r_live)
+        e_live = abs_excess(t[r_live][:, :live], ref_live[:, :live])
+        assert e_live <= OUT_ATOL, "trim: live queries err %.2e" % e_live
+    pad = t[alive][:, live:]
+    e_pad = np.minimum(np.abs(pad - o[alive][:, live:]), np.abs(pad)).max() if pad.size else 0.0
+    assert e_pad == 0, "trim: padded queries neither the untrimmed value nor zero"
+    dead = t[~alive]
+    assert (np.abs(dead).max() if dead.size else 0.0) == 0, "trim: a dead row was written"
+
+
+def test_packed_three_slots(hip):
+    """G == 3: no gate, q/k/v read in place; gate_bias may be any size."""
+    X, Y, H, D = 8, 96, 4, 32
+    p, bias, gb, km = make(X, Y, H, D, False, 0.1, Y, G=3)
+    tp, tb, tk = (torch.from_numpy(a).cuda() for a in (p, bias, km))
+    one = torch.zeros(1, dtype=torch.float16, device="cuda")
+    out = hip.attention_packed(tp, tb, tk, one, D ** -0.5, 64, 32, False)
+    o = out.float().cpu().numpy()
+    q, k, v, _ = ora.unpack(p, False)
+    ref, _ = ora.attention_fwd(q, k, v, bias, km, D ** -0.5)
+    ref = ora.repack_out(ref, False)
+    assert abs_excess(o, ref) <= OUT_ATOL
