@@ -583,7 +583,9 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     const int64_t qt = (a.Sq + Q::kBQ - 1) / Q::kBQ;
     const int64_t g1 = qt * a.H * a.N;
     if (g1 > INT32_MAX) return invalid("attention_bwd: too many work items");
+    stage_mark(stream, 0);
     hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
+    stage_mark(stream, 1);
     const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks;
     if (want_dbias) {
         if (p.dyn_lds > 64 * 1024) {
@@ -593,13 +595,17 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
         }
         hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, true>), dim3((unsigned)g2),
                            dim3(DkdvTile<DP>::kThreads), p.dyn_lds, stream, a);
+        stage_mark(stream, 2);
         const int64_t g3 = (int64_t)((a.Sq + 63) / 64) * p.kblocks * a.H;
         hipLaunchKernelGGL(attn_bwd_dbias_kernel, dim3((unsigned)g3), dim3(256), 0, stream, a);
+        stage_mark(stream, 3);
     } else {
         hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, false>), dim3((unsigned)g2),
                            dim3(DkdvTile<DP>::kThreads), 0, stream, a);
+        stage_mark(stream, 2);
         const int64_t nb = (int64_t)a.H * a.Sq * a.Sk;
         hipLaunchKernelGGL(fill_zero_f32, dim3(1024), dim3(256), 0, stream, a.dbias, nb);
+        stage_mark(stream, 3);
     }
     return launch_status("attention_bwd");
 }

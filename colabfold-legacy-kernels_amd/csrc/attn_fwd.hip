@@ -341,8 +341,10 @@ static int launch_fwd(hipStream_t stream, int device, const FwdArgs& a) {
     const int64_t grid = qt * a.H * a.N;
     if (grid == 0) return ok();
     if (grid > INT32_MAX) return invalid("attention: too many work items");
+    stage_mark(stream, 0);
     hipLaunchKernelGGL((attn_fwd_kernel<DP, LSE, GATE, TRIM>), dim3((unsigned)grid),
                        dim3(T::kThreads), 0, stream, a);
+    stage_mark(stream, 1);
     return launch_status("attention");
 }
 

@@ -9,6 +9,9 @@ namespace {
 thread_local std::string g_last_error;
 constexpr int kMaxDevices = 16;
 int g_shared_limit[kMaxDevices] = {};
+constexpr int kMaxStages = 16;
+void* g_stage_events[kMaxStages] = {};
+int g_stage_count = 0;
 
 const char* type_name(int t) {
     switch (t) {
@@ -37,6 +40,12 @@ int launch_status(const char* what) {
         return fail(CLK_INTERNAL, std::string(what) + " launch: " + hipGetErrorString(err));
     }
     return ok();
+}
+
+void stage_mark(hipStream_t s, int i) {
+    if (i < g_stage_count && g_stage_events[i] != nullptr) {
+        (void)hipEventRecord(static_cast<hipEvent_t>(g_stage_events[i]), s);
+    }
 }
 
 int shared_limit(int device) {
@@ -73,3 +82,12 @@ int check_types(const char* what, const clk_buffer* const* bufs, const int* type
 extern "C" const char* clk_last_error(void) { return clk::g_last_error.c_str(); }
 
 extern "C" const char* clk_version(void) { return "0.6.0+gfx950"; }
+
+extern "C" int clk_set_stage_events(void* const* events, int32_t count) {
+    if (count < 0 || count > clk::kMaxStages || (count > 0 && events == nullptr)) {
+        return clk::invalid("clk_set_stage_events: count must be 0.." + std::to_string(clk::kMaxStages));
+    }
+    for (int i = 0; i < clk::kMaxStages; ++i) clk::g_stage_events[i] = i < count ? events[i] : nullptr;
+    clk::g_stage_count = count;
+    return clk::ok();
+}

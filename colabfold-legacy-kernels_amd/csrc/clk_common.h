@@ -81,6 +81,9 @@ inline int invalid(const std::string& msg) { return fail(CLK_INVALID_ARGUMENT, m
 
 int launch_status(const char* what);
 
+// Records stage event i on stream s if a caller armed clk_set_stage_events with more than i.
+void stage_mark(hipStream_t s, int i);
+
 // Device LDS limit per workgroup, read once per device (a benign race, like the reference's
 // per-device caches).
 int shared_limit(int device);

@@ -839,10 +839,14 @@ extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buff
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (K == 64) {
         if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64>, grid, lds, s, &a, 0)) return st;
+        stage_mark(s, 0);
         hipLaunchKernelGGL(ln_gdp_kernel<64>, grid, dim3(kFThreads), lds, s, a);
+        stage_mark(s, 1);
     } else {
         if (int st = launch_fused("ln_gdp", ln_gdp_kernel<128>, grid, lds, s, &a, 0)) return st;
+        stage_mark(s, 0);
         hipLaunchKernelGGL(ln_gdp_kernel<128>, grid, dim3(kFThreads), lds, s, a);
+        stage_mark(s, 1);
     }
     return launch_status("ln_gdp");
 }
@@ -854,7 +858,9 @@ static int run_epilogue(const EpiArgs& a, hipStream_t s) {
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     const dim3 grid(persistent_grid(tiles, lds));
     if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, ADD>, grid, lds, s, &a, 0)) return st;
+    stage_mark(s, 0);
     hipLaunchKernelGGL((epilogue_kernel<C, CA, ADD>), grid, dim3(kFThreads), lds, s, a);
+    stage_mark(s, 1);
     return launch_status("trimul_epilogue");
 }
 
@@ -914,7 +920,9 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     const dim3 grid(persistent_grid(tiles, lds), chunks);
     if (int st = launch_fused(what, proj_kernel<K, LN>, grid, lds, s, &a, 0)) return st;
+    stage_mark(s, 0);
     hipLaunchKernelGGL((proj_kernel<K, LN>), grid, dim3(kFThreads), lds, s, a);
+    stage_mark(s, 1);
     return launch_status(what);
 }
 
@@ -1000,7 +1008,9 @@ static int run_transition(const TransArgs& a, hipStream_t s) {
     const int64_t tiles = (a.M + kTransRows - 1) / kTransRows;
     const dim3 grid(persistent_grid(tiles, lds));
     if (int st = launch_fused("transition", transition_kernel<C, ADD>, grid, lds, s, &a, 0)) return st;
+    stage_mark(s, 0);
     hipLaunchKernelGGL((transition_kernel<C, ADD>), grid, dim3(kFThreads), lds, s, a);
+    stage_mark(s, 1);
     return launch_status("transition");
 }
 

@@ -43,6 +43,12 @@ const char* clk_last_error(void);
 /* Version of this library, e.g. "0.6.0+gfx950". */
 const char* clk_version(void);
 
+/* Measurement hook, no counterpart in the reference. With count > 0, each later entry point
+ * records events[0] on its stream before its first kernel launch and events[i] after its i-th,
+ * for i < count (hipEvent_t handles, owned by the caller). count 0 turns it off. The setting is
+ * process-wide and meant for a single-threaded benchmark. */
+int clk_set_stage_events(void* const* events, int32_t count);
+
 /* ---- attention ------------------------------------------------------------------------ */
 
 /* VoltaMma (reference cuda/volta_mma_attn.cu:522-542, handler 625-640).

@@ -1,0 +1,154 @@
+"""Pins the float64 fused-op oracle (oracle/fused.py) against torch's layer_norm, explicit
+per-element sums, the transition's blocked weight layout read element by element, closed-form
+special cases, a brute-force statement of the keep rule, and the committed golden fixtures.
+CPU only.
+"""
+import os
+
+import numpy as np
+import torch
+
+from oracle import fused as orf
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+EPS = 1e-5
+
+
+def fused_inputs(seed, m=200, c=64):
+    """Tiny inputs for every fused op; keep has a computed, a padding, a skipped and a partial
+    64-row tile."""
+    rng = np.random.default_rng(seed)
+    f16 = lambda *s, a=1.0: (rng.standard_normal(s) * a).astype(np.float16).astype(np.float64)
+    f32 = lambda *s, a=1.0, mean=0.0: (rng.standard_normal(s) * a + mean).astype(np.float32).astype(np.float64)
+    keep = np.ones(m)
+    keep[64:128] = 0.0
+    keep[128:192] = -1.0
+    keep[192:196] = 0.0
+    return {
+        "x": f16(m, c, a=2.0), "sc": f32(c, a=0.1, mean=1.0), "of": f32(c, a=0.1),
+        "wpT": f16(2 * c, c, a=0.1), "bp": f16(2 * c, a=0.1), "wgT": f16(2 * c, c, a=0.1),
+        "bg": f16(2 * c, a=0.1), "mask": (rng.random(m) > 0.1).astype(np.float64),
+        "x_cm": f32(c, m, a=20.0), "lsc": f32(c, a=0.1, mean=1.0), "lof": f32(c, a=0.1),
+        "woT": f16(c, c, a=0.1), "bo": f16(c, a=0.1), "wgT2": f16(c, c, a=0.1), "bg2": f16(c, a=0.1),
+        "wT": f16(128, c, a=0.1), "wbT": f16(4, c, a=0.1), "o": f16(m, c), "res": f16(m, c, a=2.0),
+        "w1T": f16(4 * c, c, a=c ** -0.5), "b1": f16(4 * c, a=0.1),
+        "w2T": orf.w2_blocked(f16(4 * c, c, a=(4 * c) ** -0.5)), "b2": f16(c, a=0.1), "keep": keep,
+    }
+
+
+def test_layer_norm_matches_torch():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((37, 128)) * 3 + 5
+    sc, of = rng.standard_normal(128), rng.standard_normal(128)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x), (128,), torch.from_numpy(sc),
+                                          torch.from_numpy(of), EPS).numpy()
+    np.testing.assert_allclose(orf.layer_norm(x, sc, of, EPS, round_mid=False), want, rtol=1e-12, atol=1e-12)
+    # the fp16 rounding point: the rounded LN is the fp16 value of the exact one
+    np.testing.assert_array_equal(orf.layer_norm(x, sc, of, EPS), want.astype(np.float16).astype(np.float64))
+
+
+def test_tile_work_brute_force():
+    rng = np.random.default_rng(1)
+    for m, rows, other in ((200, 64, -1.0), (200, 64, 0.0), (97, 32, -1.0), (5, 64, 0.0)):
+        keep = rng.choice([-1.0, 0.0, 1.0], size=m, p=[0.5, 0.3, 0.2])
+        keep[:rows] = -1.0  # one all-negative tile
+        got = orf.tile_work(keep, m, rows, other)
+        for t, w in enumerate(got):
+            vals = [keep[r] if r < m else other for r in range(t * rows, (t + 1) * rows)]
+            want = orf.COMPUTE if any(v > 0 for v in vals) else (
+                orf.PADDING if any(v == 0 for v in vals) else orf.SKIP)
+            assert w == want, (m, rows, other, t)
+
+
+def test_w2_blocked_layout():
+    rng = np.random.default_rng(2)
+    w2 = rng.standard_normal((256, 64))
+    w2T = orf.w2_blocked(w2)
+    for j, c, i in ((0, 0, 0), (3, 63, 63), (1, 17, 5), (2, 40, 33)):
+        assert w2T[j, c, i] == w2[64 * j + i, c]
+    np.testing.assert_array_equal(orf.w2_unblocked(w2T), w2)
+
+
+def test_ln_gdp_elements():
+    inp = fused_inputs(3)
+    left, right = orf.ln_gdp(inp["x"], inp["sc"], inp["of"], inp["wpT"], inp["bp"], inp["wgT"], inp["bg"],
+                             np.ones(200), EPS)
+    y = orf.layer_norm(inp["x"], inp["sc"], inp["of"], EPS)
+    for m, n in ((0, 0), (5, 70), (199, 127), (100, 64)):
+        p = sum(y[m, k] * inp["wpT"][n, k] for k in range(64)) + inp["bp"][n]
+        g = sum(y[m, k] * inp["wgT"][n, k] for k in range(64)) + inp["bg"][n]
+        want = p / (1 + np.exp(-g))
+        got = left[n, m] if n < 64 else right[n - 64, m]
+        assert abs(got - want) < 1e-12
+
+
+def test_ln_gdp_mask_rows_and_padding():
+    inp = fused_inputs(4)
+    mask = np.ones(200)
+    mask[:64] = 0.0          # a padding tile: written as zeros
+    mask[64:128] = -1.0      # a skipped tile: not written
+    mask[130] = -2.0         # inside a computed tile: max(mask, 0) zeroes the row
+    left, right = orf.ln_gdp(inp["x"], inp["sc"], inp["of"], inp["wpT"], inp["bp"], inp["wgT"], inp["bg"], mask, EPS)
+    assert (left[:, :64] == 0).all() and np.isnan(left[:, 64:128]).all() and (left[:, 130] == 0).all()
+    assert np.isfinite(right[:, 128:]).all()
+
+
+def test_output_projection_explicit():
+    inp = fused_inputs(5)
+    out = orf.output_projection(inp["o"], inp["woT"], inp["bo"], inp["res"], None)
+    for m, n in ((0, 0), (199, 63), (77, 31)):
+        want = sum(inp["o"][m, k] * inp["woT"][n, k] for k in range(64)) + inp["bo"][n] + inp["res"][m, n]
+        assert abs(out[m, n] - want) < 1e-12
+
+
+def test_transition_special_cases():
+    inp = fused_inputs(6)
+    zero2 = np.zeros_like(inp["w2T"])
+    out = orf.transition(inp["x"], inp["sc"], inp["of"], inp["w1T"], inp["b1"], zero2, np.zeros(64), None, EPS, True)
+    np.testing.assert_array_equal(out, inp["x"])
+    zero1 = np.zeros_like(inp["w1T"])
+    out = orf.transition(inp["x"], inp["sc"], inp["of"], zero1, np.full(256, -1.0), inp["w2T"], inp["b2"], None, EPS,
+                         False)
+    np.testing.assert_array_equal(out, np.broadcast_to(inp["b2"], out.shape))
+
+
+def test_trimul_epilogue_elements():
+    inp = fused_inputs(7)
+    out = orf.trimul_epilogue(inp["x_cm"], inp["x"], inp["sc"], inp["of"], inp["lsc"], inp["lof"], inp["woT"],
+                              inp["bo"], inp["wgT2"], inp["bg2"], None, EPS, True)
+    ycol = torch.nn.functional.layer_norm(torch.from_numpy(inp["x_cm"].T.copy()), (64,),
+                                          torch.from_numpy(inp["lsc"]), torch.from_numpy(inp["lof"]), EPS).numpy()
+    ycol = ycol.astype(np.float16).astype(np.float64)
+    a = orf.layer_norm(inp["x"], inp["sc"], inp["of"], EPS)
+    for m, o in ((0, 0), (150, 63), (33, 12)):
+        lin = sum(ycol[m, c] * inp["woT"][o, c] for c in range(64)) + inp["bo"][o]
+        gate = sum(a[m, c] * inp["wgT2"][o, c] for c in range(64)) + inp["bg2"][o]
+        want = lin / (1 + np.exp(-gate)) + inp["x"][m, o]
+        assert abs(out[m, o] - want) < 1e-9
+
+
+def test_keep_padding_and_skip():
+    inp = fused_inputs(8)
+    p, b = orf.ln_projection(inp["x"], inp["sc"], inp["of"], inp["wT"], inp["wbT"], inp["keep"], EPS)
+    assert (p[64:128] == 0).all() and np.isnan(p[128:192]).all() and np.isfinite(p[192:]).all()
+    assert (b[:, 64:128] == 0).all() and np.isnan(b[:, 128:192]).all()
+    t = orf.transition(inp["x"], inp["sc"], inp["of"], inp["w1T"], inp["b1"], inp["w2T"], inp["b2"], inp["keep"],
+                       EPS, True)
+    assert np.isnan(t[64:192]).all()  # add_input: padding keeps x, which the kernel leaves unwritten
+
+
+def test_golden_fixtures():
+    f = np.load(os.path.join(GOLDEN, "fused_small.npz"))
+    inp = fused_inputs(int(f["seed"]))
+    l, r = orf.ln_gdp(inp["x"], inp["sc"], inp["of"], inp["wpT"], inp["bp"], inp["wgT"], inp["bg"], inp["mask"], EPS)
+    p, b = orf.ln_projection(inp["x"], inp["sc"], inp["of"], inp["wT"], inp["wbT"], inp["keep"], EPS)
+    got = {
+        "gdp_left": l, "gdp_right": r, "proj_p": p, "proj_bias": b,
+        "epi": orf.trimul_epilogue(inp["x_cm"], inp["x"], inp["sc"], inp["of"], inp["lsc"], inp["lof"],
+                                   inp["woT"], inp["bo"], inp["wgT2"], inp["bg2"], inp["keep"], EPS, False),
+        "outp": orf.output_projection(inp["o"], inp["woT"], inp["bo"], inp["res"], inp["keep"]),
+        "trans": orf.transition(inp["x"], inp["sc"], inp["of"], inp["w1T"], inp["b1"], inp["w2T"], inp["b2"],
+                                inp["keep"], EPS, True),
+    }
+    for name, arr in got.items():
+        np.testing.assert_allclose(arr, f[name], rtol=1e-12, atol=1e-12, equal_nan=True, err_msg=name)
