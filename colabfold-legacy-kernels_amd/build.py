@@ -24,8 +24,10 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 ARCH = "gfx950"
 
 # Packed fp32 VALU forms are kept out of the generated code (no v_pk_{add,mul,fma}_f32).
+# MFMA results stay in VGPRs (no v_accvgpr_read per use of an accumulator).
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH,
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-mllvm", "-amdgpu-mfma-vgpr-form",
              "-Wall", "-Wno-unused-result", "-Wno-unused-function"]
 
 

@@ -84,11 +84,6 @@ __device__ __forceinline__ uint4 bload_m16(const uint8_t* p, int valid, bool vec
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-__device__ __forceinline__ uint32_t bmask_byte(const uint4& m, int key) {
-    const uint32_t w = key < 4 ? m.x : key < 8 ? m.y : key < 12 ? m.z : m.w;
-    return (w >> (8 * (key & 3))) & 0xffu;
-}
-
 // ------------------------------------------------------------------------------------------
 // dQ (and delta): the forward's orientation, S^T = K Q^T and dP^T = V dO^T with a lane on one
 // query; dQ^T = K^T dS^T takes dS^T straight from registers as its B operand.
@@ -106,9 +101,10 @@ struct DqTile {
 template <int DP>
 __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
     using T = DqTile<DP>;
-    __shared__ __attribute__((aligned(16))) half_t Ks[T::kBK * T::kLd];
-    __shared__ __attribute__((aligned(16))) half_t Vs[T::kBK * T::kLd];
-    __shared__ __attribute__((aligned(16))) half_t Kt[DP * T::kTLd];
+    // two key tiles in flight: one being read by the MFMAs, the next being written
+    __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Vs2[2][T::kBK * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Kt2[2][DP * T::kTLd];
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -140,7 +136,8 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
             for (int j = 0; j < 8; ++j) part += (float)o[j] * (float)dop[qb][ks][j];
         }
         dlt[qb] = wave_xor_sum4(part);
-        lse2[qb] = in ? a.lse[nh * a.Sq + gq] : 0.f;
+        // a query past Sq gets lse2 = +inf, so its p is 0 whatever its logits
+        lse2[qb] = in ? a.lse[nh * a.Sq + gq] : INFINITY;
         if (in && g == 0) a.delta[nh * a.Sq + gq] = dlt[qb];
     }
 
@@ -150,7 +147,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
 
+    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
+
+    // K/V chunks one tile ahead; a masked key's K row is staged as zeros (its score is 0)
     half8 kreg[T::kCPT], vreg[T::kCPT];
+    bool kkeep[T::kCPT];
     const auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
@@ -160,48 +161,74 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
             const int64_t off = kbase + (int64_t)(k0 + row) * a.D + col;
             kreg[i] = ok ? bld8(a.k + off) : bzero8();
             vreg[i] = ok ? bld8(a.v + off) : bzero8();
+            kkeep[i] = ok && mrow[k0 + row] != 0;
         }
     };
-    const auto stage = [&]() {
+    const auto stage = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
             const int c = tid + i * T::kThreads;
             if (c < T::kChunks) {
                 const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-                *reinterpret_cast<half8*>(&Ks[row * T::kLd + col]) = kreg[i];
-                *reinterpret_cast<half8*>(&Vs[row * T::kLd + col]) = vreg[i];
+                const half8 kv = kkeep[i] ? kreg[i] : bzero8();
+                const int prow = perm_row(row, 16);
+                *reinterpret_cast<half8*>(&Ks2[buf][prow * T::kLd + col]) = kv;
+                *reinterpret_cast<half8*>(&Vs2[buf][prow * T::kLd + col]) = vreg[i];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) Kt[(col + j) * T::kTLd + row] = kreg[i][j];
+                for (int j = 0; j < 8; ++j)
+                    Kt2[buf][(perm_base8(col, DP / 4) + perm_off8(j)) * T::kTLd + row] = kv[j];
             }
         }
     };
 
     const float scale = a.scale;
     const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
-    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
 
-    if (a.Sk > 0) fetch(0);
-    for (int k0 = 0; k0 < a.Sk; k0 += T::kBK) {
-        __syncthreads();
-        stage();
-        __syncthreads();
-        if (k0 + T::kBK < a.Sk) fetch(k0 + T::kBK);
-
+    // bias of this lane's 16 keys k0 + 16 g .. +15, one key tile ahead of its use; a masked key
+    // or a key past Sk gets bias -inf, so its p, and with it its dS, is 0
+    BH16 bias_n[T::kQB];
+    const auto fetch_bm = [&](int k0) {
         const int kl = k0 + 16 * g;
         const int kvalid = a.Sk - kl;
-        BH16 bias16[T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
             const int gq = q0w + 16 * qb + r16;
             const int gqc = gq < a.Sq ? gq : a.Sq - 1;
-            bias16[qb] = bload_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
+            bias_n[qb] = bload_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
         }
-        const uint4 mk = bload_m16(mrow + kl, kvalid, a.mask_vec);
+        const uint32_t keep = mask_bits16(bload_m16(mrow + kl, kvalid, a.mask_vec), kvalid);
+        if (keep != 0xffffu) {
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb)
+                fill_bias16(bias_n[qb].lo, bias_n[qb].hi, keep, 0u, (half_t)(-INFINITY),
+                            (half_t)(-INFINITY));
+        }
+    };
+
+    if (a.Sk > 0) {
+        fetch(0);
+        fetch_bm(0);
+        stage(0);
+        __syncthreads();
+    }
+    for (int k0 = 0, buf = 0; k0 < a.Sk; k0 += T::kBK, buf ^= 1) {
+        const half_t* Ks = Ks2[buf];
+        const half_t* Vs = Vs2[buf];
+        const half_t* Kt = Kt2[buf];
+        const bool more = k0 + T::kBK < a.Sk;
+        BH16 bias16[T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) bias16[qb] = bias_n[qb];
+        if (more) {
+            fetch(k0 + T::kBK);
+            fetch_bm(k0 + T::kBK);
+        }
+
 
         float4v s[4][T::kQB], dp[4][T::kQB];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const int krow = 16 * (r16 >> 2) + 4 * kb + (r16 & 3);
+            const int krow = 16 * kb + r16;  // key 16 (r/4) + 4 kb + r%4
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb) {
                 s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -219,23 +246,20 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
             }
         }
 
-        // dS^T = P^T (dP^T - delta), zero on a dead logit; packed as the B operand of dQ^T
+        // dS^T = P^T (dP^T - delta), packed as the B operand of dQ^T; a dead logit has p = 0
         half8 dsb[2][T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
-            const int gq = q0w + 16 * qb + r16;
-            const bool qin = gq < a.Sq;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int kk = 4 * kb + i;
                     const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
-                    const bool alive = qin && kk < kvalid && bmask_byte(mk, kk) != 0u;
                     const float t = fmaf(s[kb][qb][i], scale, (float)b);
                     const float p = exp2_fast(fmaf(t, kLog2e, -lse2[qb]));
-                    const float ds = pin_f32(alive ? p * (dp[kb][qb][i] - dlt[qb]) : 0.f);
-                    dsb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)ds;
+                    const float ds = p * (dp[kb][qb][i] - dlt[qb]);
+                    dsb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)pin_f32(ds);
                 }
             }
         }
@@ -244,12 +268,14 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
-                const int drow = (DP / 4) * (r16 >> 2) + 4 * db + (r16 & 3);
-                const half8 kto = bld8(&Kt[drow * T::kTLd + 16 * g + 8 * kt]);
+                const half8 kto = bld8(&Kt[(16 * db + r16) * T::kTLd + 16 * g + 8 * kt]);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[kt][qb], acc[db][qb]);
             }
         }
+        // the other buffer was last read a tile ago, before the barrier that ended that tile
+        if (more) stage(buf ^ 1);
+        __syncthreads();
     }
 
 #pragma unroll
@@ -271,27 +297,33 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
 // ------------------------------------------------------------------------------------------
 // dK, dV and the dBias partials: S = Q K^T and dP = dO V^T with a lane on one key, so P and dS
 // feed dV^T = dO^T P and dK^T = Q^T dS as B operands straight from registers.
+//
+// A workgroup owns 64 keys (four key groups of 16, one wave each) and QG query groups: for each
+// batch row n of its chunk, query group qg takes query tiles qg, qg + QG, ... of 32 queries,
+// staged by its four waves into its own LDS buffers. Every dBias element (key, q) therefore has
+// one owner wave, which adds its dS in a fixed order; the query groups' dK / dV partials are
+// summed in group order through LDS at the end of each row. Loads run one tile (and K/V one row)
+// ahead of their use.
 // ------------------------------------------------------------------------------------------
-template <int DP>
+template <int DP, int QG>
 struct DkdvTile {
-    static constexpr int kWaves = 4, kThreads = kWaves * kWave;
-    static constexpr int kBK = kWaves * 16;   // keys per workgroup, 16 per wave
-    static constexpr int kBQ = 32;            // queries per tile (one contraction step)
+    static constexpr int kWaves = 4 * QG, kThreads = kWaves * kWave;
+    static constexpr int kBK = 64;                    // keys per workgroup, 16 per key group
+    static constexpr int kBQ = 32;                    // queries per tile (one contraction step)
     static constexpr int kKS = DP / 32, kDB = DP / 16;
     static constexpr int kLd = DP + 8, kTLd = kBQ + 8;
-    static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO
-    static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
-    static constexpr int kStaticLds = (2 * kBQ * kLd + 2 * DP * kTLd) * 2;
+    static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO chunks of one tile
+    static constexpr int kCPT = (kChunks + 255) / 256;
+    static constexpr int kStage = 2 * kBQ * kLd + 2 * DP * kTLd;   // halfs per query group
+    static constexpr int kStageBytes = kStage * 2 * QG;
+    static constexpr int kCombineBytes = 4 * (QG - 1) * kDB * kWave * 4 * 4;
+    static_assert(kCombineBytes <= kStageBytes, "the combine reuses the staging area");
 };
 
-template <int DP, bool DBIAS>
-__global__ __launch_bounds__(DkdvTile<DP>::kThreads) void attn_bwd_dkdv_kernel(BwdArgs a) {
-    using T = DkdvTile<DP>;
-    __shared__ __attribute__((aligned(16))) half_t Qs[T::kBQ * T::kLd];
-    __shared__ __attribute__((aligned(16))) half_t Os[T::kBQ * T::kLd];
-    __shared__ __attribute__((aligned(16))) half_t Qt[DP * T::kTLd];
-    __shared__ __attribute__((aligned(16))) half_t Ot[DP * T::kTLd];
-    extern __shared__ __attribute__((aligned(16))) float DBt[];  // [kBK][SqP]
+template <int DP, int QG, bool DBIAS>
+__global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
+    using T = DkdvTile<DP, QG>;
+    extern __shared__ __attribute__((aligned(16))) char lds_raw[];
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
     const int kblk = item % a.kblocks, rest = item / a.kblocks;
@@ -299,164 +331,239 @@ __global__ __launch_bounds__(DkdvTile<DP>::kThreads) void attn_bwd_dkdv_kernel(B
     const int n_begin = c * a.chunk;
     const int n_end = min(a.N, n_begin + a.chunk);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int kg = wave & 3, qg = wave >> 2, gtid = tid & 255;
     const int r16 = lane & 15, g = lane >> 4;
-    const int klocal = wave * 16 + r16;
+    const int klocal = kg * 16 + r16;
     const int key = kblk * T::kBK + klocal;
     const bool kin = key < a.Sk;
     const int qtiles = (a.Sq + T::kBQ - 1) / T::kBQ;
+    const int IT = (qtiles + QG - 1) / QG;
+    const int total = (n_end - n_begin) * IT;
+
+    half_t* Qs = reinterpret_cast<half_t*>(lds_raw) + qg * T::kStage;
+    half_t* Os = Qs + T::kBQ * T::kLd;
+    half_t* Qt = Os + T::kBQ * T::kLd;
+    half_t* Ot = Qt + DP * T::kTLd;
+    float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][SqP]
+    float* comb = reinterpret_cast<float*>(lds_raw);                   // between rows only
 
     if constexpr (DBIAS) {
         for (int i = tid; i < T::kBK * a.SqP; i += T::kThreads) DBt[i] = 0.f;
     }
 
-    // Q / dO tile chunks, one tile ahead
-    half8 reg[T::kCPT];
-    const auto fetch = [&](int t) {
-        const int n = n_begin + t / qtiles, q0 = (t % qtiles) * T::kBQ;
-        const int64_t base = ((int64_t)n * a.H + h) * a.Sq * a.D;
+    const float scale = a.scale;
+    const float scale_log2e = a.scale * kLog2e;
+    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
+
+    // the next tile of this query group: Q / dO chunks to stage, and this lane's queries'
+    // lse2, delta and bias at its key
+    half8 sreg[T::kCPT];
+    float l2n[8], dln[8];
+    half8 bbn;
+    const auto fetch = [&](int n, int it) {
+        const int qi = it * QG + qg, q0 = qi * T::kBQ;
+        const bool valid = qi < qtiles;
+        const int64_t nh = (int64_t)n * a.H + h, base = nh * a.Sq * a.D;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int cc = tid + i * T::kThreads;
+            const int cc = gtid + i * 256;
             const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
             const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
-            const bool ok = cc < T::kChunks && q0 + row < a.Sq && col < a.D;
+            const bool ok = valid && cc < T::kChunks && q0 + row < a.Sq && col < a.D;
             const half_t* src = which ? a.dout : a.q;
-            reg[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
+            sreg[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int gq = q0 + 8 * g + j;
+            const bool in = valid && gq < a.Sq;
+            l2n[j] = in ? a.lse[nh * a.Sq + gq] : INFINITY;  // p = 0 past Sq
+            dln[j] = in ? a.delta[nh * a.Sq + gq] : 0.f;
+            bbn[j] = (in && kin) ? a.bias[bias_h + (int64_t)gq * a.Sk + key] : (half_t)0.f;
         }
     };
-    const auto stage = [&]() {
+    const auto stage_tile = [&]() {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int cc = tid + i * T::kThreads;
+            const int cc = gtid + i * 256;
             if (cc < T::kChunks) {
                 const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
                 const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
                 half_t* rm = which ? Os : Qs;
                 half_t* tr = which ? Ot : Qt;
-                *reinterpret_cast<half8*>(&rm[row * T::kLd + col]) = reg[i];
+                *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = sreg[i];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) tr[(col + j) * T::kTLd + row] = reg[i][j];
+                for (int j = 0; j < 8; ++j)
+                    tr[(perm_base8(col, DP / 4) + perm_off8(j)) * T::kTLd + row] = sreg[i][j];
             }
         }
     };
 
-    const float scale = a.scale;
-    const float dead_logit = kMaskedLogit * kLog2e;
-    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
-    const int total = (n_end - n_begin) * qtiles;
+    // K and V of a row as the B operands (lane column = key, slots d = 32 ks + 8 g + j)
+    half8 kopn[T::kKS], vopn[T::kKS];
+    bool kaliven = false;
+    // a masked key's K is zero, so its score is 0 and its logit the masked logit (its bias below)
+    const auto fetch_kv = [&](int n) {
+        const int64_t kbase = ((int64_t)n * a.H + h) * a.Sk * a.D;
+        kaliven = kin && a.kmask[(int64_t)n * a.Sk + key] != 0;
+#pragma unroll
+        for (int ks = 0; ks < T::kKS; ++ks) {
+            const int d0 = 32 * ks + 8 * g;
+            const bool ok = kin && d0 < a.D;
+            kopn[ks] = ok && kaliven ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
+            vopn[ks] = ok ? bld8(a.v + kbase + (int64_t)key * a.D + d0) : bzero8();
+        }
+    };
 
     half8 kop[T::kKS], vop[T::kKS];
     bool kalive = false;
     float4v accv[T::kDB], acck[T::kDB];
 
-    if (total > 0) fetch(0);
-    for (int t = 0; t < total; ++t) {
-        const int n = n_begin + t / qtiles, qi = t % qtiles, q0 = qi * T::kBQ;
-        const int64_t nh = (int64_t)n * a.H + h;
-        if (qi == 0) {
-            // this row's K and V as the B operands, lane column = key, slots d = 32 ks + 8 g + j
-            const int64_t kbase = nh * a.Sk * a.D;
+    if (total > 0) {
+        fetch(n_begin, 0);
+        fetch_kv(n_begin);
+    }
+    for (int t = 0, it = 0, n = n_begin; t < total; ++t) {
+        const int qi = it * QG + qg, q0 = qi * T::kBQ;
+        const bool valid = qi < qtiles;
+        if (it == 0) {
 #pragma unroll
             for (int ks = 0; ks < T::kKS; ++ks) {
-                const int d0 = 32 * ks + 8 * g;
-                const bool ok = kin && d0 < a.D;
-                kop[ks] = ok ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
-                vop[ks] = ok ? bld8(a.v + kbase + (int64_t)key * a.D + d0) : bzero8();
+                kop[ks] = kopn[ks];
+                vop[ks] = vopn[ks];
             }
-            kalive = kin && a.kmask[(int64_t)n * a.Sk + key] != 0;
+            kalive = kaliven;
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
                 accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
                 acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
             }
+            if (n + 1 < n_end) fetch_kv(n + 1);
         }
 
-        __syncthreads();
-        stage();
-        __syncthreads();
-        if (t + 1 < total) fetch(t + 1);
-
-        // queries q0 + 8 g + j of this lane: their lse2, delta and bias at this lane's key
-        float l2[8], dl[8], bb[8];
+        __syncthreads();  // this group's previous tile (and the last row's combine) are done
+        stage_tile();
+        // p = exp2(s scale log2e + bl), bl = (bias or the masked logit) log2e - lse2
+        float bl[8], dl[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int gq = q0 + 8 * g + j;
-            const bool in = gq < a.Sq;
-            l2[j] = in ? a.lse[nh * a.Sq + gq] : 0.f;
-            dl[j] = in ? a.delta[nh * a.Sq + gq] : 0.f;
-            bb[j] = (in && kin) ? (float)a.bias[bias_h + (int64_t)gq * a.Sk + key] : 0.f;
+            bl[j] = (kalive ? (float)bbn[j] : kMaskedLogit) * kLog2e - l2n[j];
+            dl[j] = dln[j];
+        }
+        __syncthreads();
+        if (t + 1 < total) {
+            const bool wrap = it + 1 == IT;
+            fetch(wrap ? n + 1 : n, wrap ? 0 : it + 1);
         }
 
-        // S and dP: A row r of query block qb is query 8 (r/4) + 4 qb + r%4 of the tile
-        float4v s[2], dp[2];
+        if (valid) {
+            // S and dP: A row r of query block qb is query 8 (r/4) + 4 qb + r%4 of the tile
+            float4v s[2], dp[2];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const int qrow = 8 * (r16 >> 2) + 4 * qb + (r16 & 3);
-            s[qb] = float4v{0.f, 0.f, 0.f, 0.f};
-            dp[qb] = float4v{0.f, 0.f, 0.f, 0.f};
+            for (int qb = 0; qb < 2; ++qb) {
+                const int qrow = 16 * qb + r16;  // query 8 (r/4) + 4 qb + r%4
+                s[qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                dp[qb] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < T::kKS; ++ks) {
-                const half8 qa = bld8(&Qs[qrow * T::kLd + 32 * ks + 8 * g]);
-                const half8 oa = bld8(&Os[qrow * T::kLd + 32 * ks + 8 * g]);
-                s[qb] = mfma16x16x32(qa, kop[ks], s[qb]);
-                dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
-            }
-        }
-
-        // lane holds query q0 + 8 g + 4 qb + i of its key: slot j = 4 qb + i
-        half8 pb, dsb;
-        float dsf[8];
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = 4 * qb + i;
-                const bool alive = kalive && q0 + 8 * g + j < a.Sq;
-                const float s2 = alive ? fmaf(s[qb][i], scale, bb[j]) * kLog2e : dead_logit;
-                const float p = exp2_fast(s2 - l2[j]);
-                const float ds = pin_f32(alive ? p * (dp[qb][i] - dl[j]) : 0.f);
-                pb[j] = (half_t)p;
-                dsb[j] = (half_t)ds;
-                dsf[j] = ds;
-            }
-        }
-
-        // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4
-#pragma unroll
-        for (int db = 0; db < T::kDB; ++db) {
-            const int drow = (DP / 4) * (r16 >> 2) + 4 * db + (r16 & 3);
-            const half8 ot = bld8(&Ot[drow * T::kTLd + 8 * g]);
-            const half8 qt = bld8(&Qt[drow * T::kTLd + 8 * g]);
-            accv[db] = mfma16x16x32(ot, pb, accv[db]);
-            acck[db] = mfma16x16x32(qt, dsb, acck[db]);
-        }
-
-        if constexpr (DBIAS) {
-            float* row = DBt + klocal * a.SqP + q0 + 8 * g;
-            float4 lo = *reinterpret_cast<float4*>(row);
-            float4 hi = *reinterpret_cast<float4*>(row + 4);
-            lo.x += dsf[0]; lo.y += dsf[1]; lo.z += dsf[2]; lo.w += dsf[3];
-            hi.x += dsf[4]; hi.y += dsf[5]; hi.z += dsf[6]; hi.w += dsf[7];
-            *reinterpret_cast<float4*>(row) = lo;
-            *reinterpret_cast<float4*>(row + 4) = hi;
-        }
-
-        if (qi == qtiles - 1 && kin) {
-            // lane holds d = (DP/4) g .. +DP/4 of its key
-            const int64_t off = nh * a.Sk * a.D + (int64_t)key * a.D;
-#pragma unroll
-            for (int cc = 0; cc < DP / 32; ++cc) {
-                const int d0 = (DP / 4) * g + 8 * cc;
-                if (d0 >= a.D) continue;
-                half8 ok, ov;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
-                    ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
+                for (int ks = 0; ks < T::kKS; ++ks) {
+                    const half8 qa = bld8(&Qs[qrow * T::kLd + 32 * ks + 8 * g]);
+                    const half8 oa = bld8(&Os[qrow * T::kLd + 32 * ks + 8 * g]);
+                    s[qb] = mfma16x16x32(qa, kop[ks], s[qb]);
+                    dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
                 }
-                *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
-                *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
             }
+
+            // lane holds query q0 + 8 g + 4 qb + i of its key: slot j = 4 qb + i
+            half8 pb, dsb;
+            float dsf[8];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = 4 * qb + i;
+                    const float p = exp2_fast(fmaf(s[qb][i], scale_log2e, bl[j]));
+                    const float ds = pin_f32(kalive ? p * (dp[qb][i] - dl[j]) : 0.f);
+                    pb[j] = (half_t)p;
+                    dsb[j] = (half_t)ds;
+                    dsf[j] = ds;
+                }
+            }
+
+            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4
+#pragma unroll
+            for (int db = 0; db < T::kDB; ++db) {
+                const int drow = 16 * db + r16;  // d (DP/4)(r/4) + 4 db + r%4
+                const half8 ot = bld8(&Ot[drow * T::kTLd + 8 * g]);
+                const half8 qt = bld8(&Qt[drow * T::kTLd + 8 * g]);
+                accv[db] = mfma16x16x32(ot, pb, accv[db]);
+                acck[db] = mfma16x16x32(qt, dsb, acck[db]);
+            }
+
+            if constexpr (DBIAS) {
+                float* row = DBt + klocal * a.SqP + q0 + 8 * g;
+                float4 lo = *reinterpret_cast<float4*>(row);
+                float4 hi = *reinterpret_cast<float4*>(row + 4);
+                lo.x += dsf[0]; lo.y += dsf[1]; lo.z += dsf[2]; lo.w += dsf[3];
+                hi.x += dsf[4]; hi.y += dsf[5]; hi.z += dsf[6]; hi.w += dsf[7];
+                *reinterpret_cast<float4*>(row) = lo;
+                *reinterpret_cast<float4*>(row + 4) = hi;
+            }
+        }
+
+        if (it == IT - 1) {
+            if constexpr (QG > 1) {
+                // the query groups' partials, summed in group order by group 0 (two rounds)
+                float* slot = comb + ((kg * (QG - 1) + qg - 1) * T::kDB) * 256 + lane * 4;
+                __syncthreads();
+                if (qg > 0) {
+#pragma unroll
+                    for (int db = 0; db < T::kDB; ++db) *reinterpret_cast<float4v*>(slot + db * 256) = acck[db];
+                }
+                __syncthreads();
+                if (qg == 0) {
+#pragma unroll
+                    for (int o = 0; o < QG - 1; ++o)
+#pragma unroll
+                        for (int db = 0; db < T::kDB; ++db)
+                            acck[db] += *reinterpret_cast<const float4v*>(
+                                comb + ((kg * (QG - 1) + o) * T::kDB + db) * 256 + lane * 4);
+                }
+                __syncthreads();
+                if (qg > 0) {
+#pragma unroll
+                    for (int db = 0; db < T::kDB; ++db) *reinterpret_cast<float4v*>(slot + db * 256) = accv[db];
+                }
+                __syncthreads();
+                if (qg == 0) {
+#pragma unroll
+                    for (int o = 0; o < QG - 1; ++o)
+#pragma unroll
+                        for (int db = 0; db < T::kDB; ++db)
+                            accv[db] += *reinterpret_cast<const float4v*>(
+                                comb + ((kg * (QG - 1) + o) * T::kDB + db) * 256 + lane * 4);
+                }
+            }
+            if (qg == 0 && kin) {
+                // lane holds d = (DP/4) g .. +DP/4 of its key
+                const int64_t off = ((int64_t)n * a.H + h) * a.Sk * a.D + (int64_t)key * a.D;
+#pragma unroll
+                for (int cc = 0; cc < DP / 32; ++cc) {
+                    const int d0 = (DP / 4) * g + 8 * cc;
+                    if (d0 >= a.D) continue;
+                    half8 ok, ov;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
+                        ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
+                    }
+                    *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
+                    *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
+                }
+            }
+        }
+        if (++it == IT) {
+            it = 0;
+            ++n;
         }
     }
 
@@ -537,44 +644,93 @@ static int cu_count(int device) {
 
 struct BwdPlan {
     int DP = 32;
+    int QG = 1;  // query groups of the dK/dV kernel
     int SqP = 0, kblocks = 0, chunk = 0, chunks = 0;
-    size_t dyn_lds = 0;
+    size_t stage_lds = 0, dbias_lds = 0;
     size_t delta_bytes = 0, partial_bytes = 0;
     std::string error;
 };
 
 static size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
 
-static int dkdv_static_lds(int DP) {
-    return DP == 32 ? DkdvTile<32>::kStaticLds
-                    : DP == 64 ? DkdvTile<64>::kStaticLds : DkdvTile<96>::kStaticLds;
+static size_t dkdv_stage_bytes(int DP, int QG) {
+#define CLK_STAGE(D_, Q_) if (DP == D_ && QG == Q_) return DkdvTile<D_, Q_>::kStageBytes;
+    CLK_STAGE(32, 4) CLK_STAGE(32, 2) CLK_STAGE(32, 1) CLK_STAGE(64, 2) CLK_STAGE(64, 1)
+    CLK_STAGE(96, 2) CLK_STAGE(96, 1)
+#undef CLK_STAGE
+    return 0;
 }
 
+// The dK/dV kernel's shape depends only on the problem and the device, never on want_dbias, so
+// dk and dv are bit-identical with and without dbias.
 static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
     BwdPlan p;
     p.DP = D <= 32 ? 32 : D <= 64 ? 64 : 96;
     // rows cover whole 64-query tiles of the reduce kernel; +4 floats staggers LDS banks
     p.SqP = (int)(((Sq + 63) / 64) * 64 + 4);
     p.kblocks = (int)((Sk + 63) / 64);
-    p.dyn_lds = (size_t)64 * p.SqP * sizeof(float);
+    p.dbias_lds = (size_t)64 * p.SqP * sizeof(float);
     const int limit = shared_limit(device);
-    const size_t per_wg = p.dyn_lds + dkdv_static_lds(p.DP);
-    if (limit > 0 && per_wg > (size_t)limit) {
-        p.error = "attention_bwd: dbias needs " + std::to_string(per_wg / 1024) +
+    const int qg_max = p.DP == 32 ? 4 : 2;
+    p.QG = 0;
+    for (int qg = qg_max; qg >= 1; qg /= 2) {
+        const size_t need = dkdv_stage_bytes(p.DP, qg) + p.dbias_lds;
+        if (limit <= 0 || need <= (size_t)limit) {
+            p.QG = qg;
+            break;
+        }
+    }
+    if (p.QG == 0) {
+        p.QG = 1;
+        const size_t need = dkdv_stage_bytes(p.DP, 1) + p.dbias_lds;
+        p.error = "attention_bwd: dbias needs " + std::to_string(need / 1024) +
                   " KB shared, device allows " + std::to_string(limit / 1024) + " KB";
     }
-    // enough workgroups to fill the chip once at the occupancy LDS allows
-    const int per_cu = limit > 0 ? std::max(1, std::min(4, (int)(limit / std::max<size_t>(per_wg, 1)))) : 1;
-    const int64_t target = (int64_t)cu_count(device) * per_cu;
-    const int64_t cols = H * p.kblocks;
-    int64_t chunks = cols > 0 ? std::max<int64_t>(1, target / cols) : 1;
-    chunks = std::min<int64_t>(chunks, std::max<int64_t>(N, 1));
-    p.chunk = (int)((N + chunks - 1) / std::max<int64_t>(chunks, 1));
+    p.stage_lds = dkdv_stage_bytes(p.DP, p.QG);
+    // batch-row chunks: the fewest rounds of workgroups times rows per workgroup
+    const size_t per_wg = p.stage_lds + p.dbias_lds;
+    const int threads = 256 * p.QG;
+    int per_cu = std::max(1, std::min(2048 / threads, limit > 0 ? (int)(limit / per_wg) : 1));
+    const int64_t slots = (int64_t)cu_count(device) * per_cu;
+    const int64_t cols = std::max<int64_t>(H * p.kblocks, 1);
+    int64_t best = 1, best_cost = INT64_MAX;
+    for (int64_t ch = 1; ch <= std::max<int64_t>(N, 1); ++ch) {
+        const int64_t rows = (N + ch - 1) / ch;
+        const int64_t real = (N + rows - 1) / rows;
+        const int64_t rounds = (real * cols + slots - 1) / slots;
+        // each extra chunk adds a dbias partial to write and sum; a row costs about 24 of them
+        const int64_t cost = rounds * rows * 24 + real;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = real;
+        }
+    }
+    p.chunk = (int)((N + best - 1) / best);
     if (p.chunk <= 0) p.chunk = 1;
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
     p.delta_bytes = round256((size_t)N * H * Sq * sizeof(float));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * 64 * p.SqP * sizeof(float));
     return p;
+}
+
+template <int DP, int QG>
+static void launch_dkdv(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bool want_dbias) {
+    using T = DkdvTile<DP, QG>;
+    const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks;
+    const size_t lds = p.stage_lds + (want_dbias ? p.dbias_lds : 0);
+    const void* fn = want_dbias ? reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DP, QG, true>)
+                                : reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DP, QG, false>);
+    if (lds > 64 * 1024) {
+        // LDS past 64 KB per workgroup is opt-in on some runtimes; a failure shows at launch
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    }
+    if (want_dbias) {
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, QG, true>), dim3((unsigned)g2), dim3(T::kThreads),
+                           lds, stream, a);
+    } else {
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, QG, false>), dim3((unsigned)g2), dim3(T::kThreads),
+                           lds, stream, a);
+    }
 }
 
 template <int DP>
@@ -586,27 +742,22 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     stage_mark(stream, 0);
     hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
     stage_mark(stream, 1);
-    const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks;
+    if (p.QG == 4) {
+        if constexpr (DP == 32) launch_dkdv<DP, 4>(stream, a, p, want_dbias);
+    } else if (p.QG == 2) {
+        launch_dkdv<DP, 2>(stream, a, p, want_dbias);
+    } else {
+        launch_dkdv<DP, 1>(stream, a, p, want_dbias);
+    }
+    stage_mark(stream, 2);
     if (want_dbias) {
-        if (p.dyn_lds > 64 * 1024) {
-            // LDS past 64 KB per workgroup is opt-in on some runtimes; failure shows at launch
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DP, true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.dyn_lds);
-        }
-        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, true>), dim3((unsigned)g2),
-                           dim3(DkdvTile<DP>::kThreads), p.dyn_lds, stream, a);
-        stage_mark(stream, 2);
         const int64_t g3 = (int64_t)((a.Sq + 63) / 64) * p.kblocks * a.H;
         hipLaunchKernelGGL(attn_bwd_dbias_kernel, dim3((unsigned)g3), dim3(256), 0, stream, a);
-        stage_mark(stream, 3);
     } else {
-        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<DP, false>), dim3((unsigned)g2),
-                           dim3(DkdvTile<DP>::kThreads), 0, stream, a);
-        stage_mark(stream, 2);
         const int64_t nb = (int64_t)a.H * a.Sq * a.Sk;
         hipLaunchKernelGGL(fill_zero_f32, dim3(1024), dim3(256), 0, stream, a.dbias, nb);
-        stage_mark(stream, 3);
     }
+    stage_mark(stream, 3);
     return launch_status("attention_bwd");
 }
 

@@ -49,7 +49,7 @@ struct FwdTile {
     static constexpr int kVtLd = kBK + 8;             // V^T row stride in LDS (halfs)
     static constexpr int kChunks = kBK * DP / 8;      // 16-byte chunks in a K (or V) tile
     static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
-    static constexpr int kLds = (kBK * kKsLd + DP * kVtLd) * 2;
+    static constexpr int kLds = 2 * (kBK * kKsLd + DP * kVtLd) * 2;
 };
 
 struct H16 {
@@ -92,20 +92,12 @@ __device__ __forceinline__ uint4 load_m16(const uint8_t* p, int valid, bool vec)
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-__device__ __forceinline__ bool all_bytes_set(uint32_t w) {
-    return ((w - 0x01010101u) & ~w & 0x80808080u) == 0u;
-}
-
-__device__ __forceinline__ uint32_t mask_byte(const uint4& m, int key) {
-    const uint32_t w = key < 4 ? m.x : key < 8 ? m.y : key < 12 ? m.z : m.w;
-    return (w >> (8 * (key & 3))) & 0xffu;
-}
-
 template <int DP, bool LSE, bool GATE, bool TRIM>
 __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs a) {
     using T = FwdTile<DP>;
-    __shared__ __attribute__((aligned(16))) half_t Ks[T::kBK * T::kKsLd];
-    __shared__ __attribute__((aligned(16))) half_t Vt[DP * T::kVtLd];
+    // two key tiles in flight: one being read by the MFMAs, the next being written
+    __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kKsLd];
+    __shared__ __attribute__((aligned(16))) half_t Vt2[2][DP * T::kVtLd];
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -159,8 +151,13 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         for (int db = 0; db < T::kDB; ++db) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    // K/V tile chunks held in registers one tile ahead of their LDS store
+    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
+
+    // K/V tile chunks held in registers one tile ahead of their LDS store, with their key's mask:
+    // a masked key's K row is staged as zeros, so its score is exactly 0 and its bias register
+    // (which then holds the masked logit) is its logit
     half8 kreg[T::kCPT], vreg[T::kCPT];
+    bool kkeep[T::kCPT];
     const auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
@@ -170,90 +167,114 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
             const int64_t off = kbase + (int64_t)(k0 + row) * a.ks + col;
             kreg[i] = ok ? ld8(a.k + off) : zero8();
             vreg[i] = ok ? ld8(a.v + off) : zero8();
+            kkeep[i] = ok && mrow[k0 + row] != 0;
         }
     };
-    const auto stage = [&]() {
+    const auto stage = [&](int buf) {
+        half_t* Ks = Ks2[buf];
+        half_t* Vt = Vt2[buf];
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
             const int c = tid + i * T::kThreads;
             if (c < T::kChunks) {
                 const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-                *reinterpret_cast<half8*>(&Ks[row * T::kKsLd + col]) = kreg[i];
+                *reinterpret_cast<half8*>(&Ks[perm_row(row, 16) * T::kKsLd + col]) =
+                    kkeep[i] ? kreg[i] : zero8();
 #pragma unroll
-                for (int j = 0; j < 8; ++j) Vt[(col + j) * T::kVtLd + row] = vreg[i][j];
+                for (int j = 0; j < 8; ++j)
+                    Vt[(perm_base8(col, DP / 4) + perm_off8(j)) * T::kVtLd + row] = vreg[i][j];
             }
         }
     };
 
     const float scale = a.scale;
     const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
-    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
 
-    if (k_end > 0) fetch(0);
-    for (int k0 = 0; k0 < k_end; k0 += T::kBK) {
-        __syncthreads();
-        stage();
-        __syncthreads();
-        if (k0 + T::kBK < k_end) fetch(k0 + T::kBK);
-
-        // this lane's 16 keys k0 + 16 g .. +15: bias of its queries and the mask
+    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, one key tile ahead of its
+    // use; a masked key's bias becomes the masked logit -1e4, a key past Sk's -inf
+    H16 bias_n[T::kQB];
+    const auto fetch_bm = [&](int k0) {
         const int kl = k0 + 16 * g;
         const int kvalid = a.Sk - kl;
-        H16 bias16[T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
             const int gq = q0w + 16 * qb + r16;
             const int gqc = gq < a.Sq ? gq : a.Sq - 1;
-            bias16[qb] = load_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
+            bias_n[qb] = load_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
         }
-        const uint4 mk = load_m16(mrow + kl, kvalid, a.mask_vec);
-        const bool kept = kvalid >= 16 && all_bytes_set(mk.x) && all_bytes_set(mk.y) &&
-                          all_bytes_set(mk.z) && all_bytes_set(mk.w);
-        const bool fast = __all(kept);
+        const uint32_t keep = mask_bits16(load_m16(mrow + kl, kvalid, a.mask_vec), kvalid);
+        if (keep != 0xffffu) {
+            const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb)
+                fill_bias16(bias_n[qb].lo, bias_n[qb].hi, keep, inside, (half_t)kMaskedLogit,
+                            (half_t)(-INFINITY));
+        }
+    };
+
+    if (k_end > 0) {
+        fetch(0);
+        fetch_bm(0);
+        stage(0);
+        __syncthreads();
+    }
+    for (int k0 = 0, buf = 0; k0 < k_end; k0 += T::kBK, buf ^= 1) {
+        const half_t* Ks = Ks2[buf];
+        const half_t* Vt = Vt2[buf];
+        const bool more = k0 + T::kBK < k_end;
+        H16 bias16[T::kQB];
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) bias16[qb] = bias_n[qb];
+        if (more) {
+            fetch(k0 + T::kBK);
+            fetch_bm(k0 + T::kBK);
+        }
 
         // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4
         float4v s[4][T::kQB];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const int krow = 16 * (r16 >> 2) + 4 * kb + (r16 & 3);
+            // key 16 (r/4) + 4 kb + r%4, stored at row 16 kb + r
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < T::kKS; ++ks) {
-                const half8 kop = ld8(&Ks[krow * T::kKsLd + 32 * ks + 8 * g]);
+                const half8 kop = ld8(&Ks[(16 * kb + r16) * T::kKsLd + 32 * ks + 8 * g]);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
             }
         }
 
-        // natural-domain logits t = scale s + bias; masked keys -1e4, keys past Sk -inf
+        // natural-domain logits t = scale s + bias: a masked key's s is 0 and its bias the masked
+        // logit, a key past Sk has bias -inf
         float m_tile[T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
             float mx = -INFINITY;
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
+            for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int kk = 4 * kb + i;
                     const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
-                    float t = fmaf(s[kb][qb][i], scale, (float)b);
-                    if (!fast) {
-                        const bool in = kk < kvalid;
-                        t = (in && mask_byte(mk, kk) != 0u) ? t : (in ? kMaskedLogit : -INFINITY);
-                    }
+                    const float t = fmaf(s[kb][qb][i], scale, (float)b);
                     s[kb][qb][i] = t;
                     mx = fmaxf(mx, t);
                 }
-            }
-            m_tile[qb] = wave_xor_max4(mx);
+            m_tile[qb] = mx;
         }
 
-        // lazy max: move only when some query of the wave gains more than 6 in log2 units
+        // lazy max: move only when some query of the wave gains more than 6 in log2 units. A
+        // query's tile max is the largest of its four lanes' maxima, so the per-lane test decides
+        // the same; the cross-lane maximum is only needed on a tile that raises.
         bool up = false;
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) up |= m_tile[qb] * kLog2e > m_run[qb] * kLog2e + 6.f;
         const bool raise = __any(up);
+        if (raise) {
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) m_tile[qb] = wave_xor_max4(m_tile[qb]);
+        }
 
         half8 pb[2][T::kQB];
 #pragma unroll
@@ -285,12 +306,14 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
-                const int drow = (DP / 4) * (r16 >> 2) + 4 * db + (r16 & 3);
-                const half8 vop = ld8(&Vt[drow * T::kVtLd + 16 * g + 8 * kt]);
+                const half8 vop = ld8(&Vt[(16 * db + r16) * T::kVtLd + 16 * g + 8 * kt]);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(vop, pb[kt][qb], acc[db][qb]);
             }
         }
+        // the other buffer was last read a tile ago, before the barrier that ended that tile
+        if (more) stage(buf ^ 1);
+        __syncthreads();
     }
 
     // epilogue: lane g holds d = (DP/4) g .. +DP/4 of query q0w + 16 qb + r16

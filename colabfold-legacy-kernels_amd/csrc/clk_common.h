@@ -35,6 +35,18 @@ __device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// LDS row of tile row x, for operand tiles whose A row r of block b is
+//   x = per (r / 4) + 4 b + r % 4:
+// stored at row 16 b + r, a 16-lane group reads 16 consecutive rows, which with a row stride of
+// 20 (mod 64) words or 36 words falls on 16 disjoint groups of four LDS banks.
+__device__ __forceinline__ int perm_row(int x, int per) {
+    return 16 * ((x % per) >> 2) + 4 * (x / per) + (x & 3);
+}
+// perm_row(col + j, per) for col a multiple of 8, j < 8 and per a multiple of 8: a per-lane base
+// plus a compile-time offset for each j.
+__device__ __forceinline__ int perm_base8(int col, int per) { return 4 * (col % per) + 4 * (col / per); }
+__host__ __device__ constexpr int perm_off8(int j) { return 16 * (j >> 2) + (j & 3); }
+
 // Pin v as an fp32 register value, so its later rounding to fp16 is a separate step that the
 // compiler cannot fold into the multiply producing v (v_fma_mixlo_f16 rounds once). Every
 // template variant of a kernel then rounds alike, as the reference rounds its fp32 dS.
@@ -46,6 +58,39 @@ __device__ __forceinline__ float pin_f32(float v) {
 // sigmoid(g) = 1 / (1 + 2^(-g log2 e)), one v_exp_f32 and one v_rcp_f32
 __device__ __forceinline__ float sigmoid_fast(float g) {
     return __builtin_amdgcn_rcpf(1.0f + exp2_fast(-kLog2e * g));
+}
+
+// 16 bits, one per byte of m (16 mask bytes), set where the byte is nonzero and its index is
+// below `valid`.
+__device__ __forceinline__ uint32_t mask_bits16(uint4 m, int valid) {
+    const uint32_t w[4] = {m.x, m.y, m.z, m.w};
+    uint32_t bits = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // high bit of each byte set where that byte is nonzero
+        const uint32_t hi = ((w[q] & 0x7f7f7f7fu) + 0x7f7f7f7fu | w[q]) & 0x80808080u;
+        bits |= ((hi >> 7) & 1u) << (4 * q);
+        bits |= ((hi >> 15) & 1u) << (4 * q + 1);
+        bits |= ((hi >> 23) & 1u) << (4 * q + 2);
+        bits |= ((hi >> 31) & 1u) << (4 * q + 3);
+    }
+    const uint32_t in = valid >= 16 ? 0xffffu : valid <= 0 ? 0u : (1u << valid) - 1u;
+    return bits & in;
+}
+
+// Bias values of 16 consecutive keys (lo = keys 0..7, hi = 8..15) with key kk replaced by
+// `masked` where its keep bit is clear but it lies inside Sk, and by `outside` past Sk.
+__device__ __forceinline__ void fill_bias16(half8& lo, half8& hi, uint32_t keep, uint32_t inside,
+                                            half_t masked, half_t outside) {
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+        const half_t f = (inside >> kk) & 1u ? masked : outside;
+        if (kk < 8) {
+            lo[kk] = (keep >> kk) & 1u ? lo[kk] : f;
+        } else {
+            hi[kk - 8] = (keep >> kk) & 1u ? hi[kk - 8] : f;
+        }
+    }
 }
 
 __device__ __forceinline__ float wave_xor_sum4(float v) {
