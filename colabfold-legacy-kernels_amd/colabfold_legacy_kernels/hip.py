@@ -152,10 +152,15 @@ def attention_bwd_workspace(q, k):
                                                       _ref(buffer(k))))
 
 
-def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, want_dbias=True, workspace=None):
-    """VoltaMmaBwd: dq, dk, dv F16 and dbias [H,Sq,Sk] F32 (zeros without want_dbias)."""
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    dbias = torch.empty(bias.shape, dtype=torch.float32, device=q.device)
+def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, want_dbias=True, workspace=None,
+                  grads=None):
+    """VoltaMmaBwd: dq, dk, dv F16 and dbias [H,Sq,Sk] F32 (zeros without want_dbias), written
+    into `grads` = (dq, dk, dv, dbias) when given, as into XLA's preallocated results."""
+    if grads is None:
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dbias = torch.empty(bias.shape, dtype=torch.float32, device=q.device)
+    else:
+        dq, dk, dv, dbias = grads
     if workspace is None:
         need = attention_bwd_workspace(q, k)
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)

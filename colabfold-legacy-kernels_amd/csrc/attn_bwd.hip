@@ -10,8 +10,11 @@
 //
 // Where the reference adds dQ and dBias with fp32 atomics into global memory, this backward is
 // three kernels with no atomics, so every result is bit-identical from run to run:
+//   biast_kernel  bias * log2e as fp32, transposed to [H][keys][queries] and zero-padded, so a
+//                 dK/dV lane reads its eight queries' bias at its key with two vector loads.
 //   dq_kernel     one workgroup per (n, h, 128 queries), looping over key tiles as the forward
-//                 does: dQ^T = K^T dS^T accumulates in registers; it also writes delta.
+//                 does: dQ^T = K^T dS^T accumulates in registers; it also writes delta and lse2
+//                 padded to whole 32-query tiles (0 and +inf past Sq).
 //   dkdv_kernel   one workgroup per (h, 64 keys, chunk of batch rows): for each row n of its
 //                 chunk it loops over query tiles, dV^T = dO^T P and dK^T = Q^T dS accumulate in
 //                 registers, and each wave adds its 16 keys' dS into an fp32 [64 keys][Sq] dBias
@@ -35,9 +38,12 @@ struct BwdArgs {
     half_t* dk;
     half_t* dv;
     float* dbias;
-    float* delta;    // workspace [N, H, Sq]
+    float* delta;    // workspace [N, H, SqA]: rowsum(out * dout), 0 past Sq
+    float* lse2p;    // workspace [N, H, SqA]: lse, +inf past Sq
+    float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside
     float* partial;  // workspace [chunks][H][kblocks][64][SqP]
     int N, H, Sq, Sk, D;
+    int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
     int SqP;         // partial row stride (floats)
     int kblocks;     // ceil(Sk / 64)
     int chunk;       // batch rows per dkdv workgroup
@@ -138,7 +144,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
         dlt[qb] = wave_xor_sum4(part);
         // a query past Sq gets lse2 = +inf, so its p is 0 whatever its logits
         lse2[qb] = in ? a.lse[nh * a.Sq + gq] : INFINITY;
-        if (in && g == 0) a.delta[nh * a.Sq + gq] = dlt[qb];
+        if (gq < a.SqA && g == 0) {
+            a.delta[nh * a.SqA + gq] = in ? dlt[qb] : 0.f;
+            a.lse2p[nh * a.SqA + gq] = lse2[qb];
+        }
     }
 
     float4v acc[T::kDB][T::kQB];
@@ -353,14 +362,16 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     const float scale = a.scale;
     const float scale_log2e = a.scale * kLog2e;
-    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
+    const float* bias_row = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
 
-    // the next tile of this query group: Q / dO chunks to stage, and this lane's queries'
-    // lse2, delta and bias at its key
-    half8 sreg[T::kCPT];
-    float l2n[8], dln[8];
-    half8 bbn;
-    const auto fetch = [&](int n, int it) {
+    // the next tile of this query group: Q / dO chunks to stage, and this lane's eight queries'
+    // lse2, delta and log2e-scaled bias at its key (padded past Sq: lse2 +inf, delta 0)
+    struct Pre {
+        half8 s[T::kCPT];
+        float l2[8], dl[8], bt[8];
+    };
+    Pre pre;
+    const auto fetch = [&](Pre& d, int n, int it) {
         const int qi = it * QG + qg, q0 = qi * T::kBQ;
         const bool valid = qi < qtiles;
         const int64_t nh = (int64_t)n * a.H + h, base = nh * a.Sq * a.D;
@@ -371,18 +382,26 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
             const bool ok = valid && cc < T::kChunks && q0 + row < a.Sq && col < a.D;
             const half_t* src = which ? a.dout : a.q;
-            sreg[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
+            d.s[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int gq = q0 + 8 * g + j;
-            const bool in = valid && gq < a.Sq;
-            l2n[j] = in ? a.lse[nh * a.Sq + gq] : INFINITY;  // p = 0 past Sq
-            dln[j] = in ? a.delta[nh * a.Sq + gq] : 0.f;
-            bbn[j] = (in && kin) ? a.bias[bias_h + (int64_t)gq * a.Sk + key] : (half_t)0.f;
+        if (valid) {
+            const float* l2p = a.lse2p + nh * a.SqA + q0 + 8 * g;
+            const float* dlp = a.delta + nh * a.SqA + q0 + 8 * g;
+            const float4 l2a = *reinterpret_cast<const float4*>(l2p);
+            const float4 l2b = *reinterpret_cast<const float4*>(l2p + 4);
+            const float4 dla = *reinterpret_cast<const float4*>(dlp);
+            const float4 dlb = *reinterpret_cast<const float4*>(dlp + 4);
+            const float4 bta = *reinterpret_cast<const float4*>(bias_row + q0);
+            const float4 btb = *reinterpret_cast<const float4*>(bias_row + q0 + 4);
+            d.l2[0] = l2a.x; d.l2[1] = l2a.y; d.l2[2] = l2a.z; d.l2[3] = l2a.w;
+            d.l2[4] = l2b.x; d.l2[5] = l2b.y; d.l2[6] = l2b.z; d.l2[7] = l2b.w;
+            d.dl[0] = dla.x; d.dl[1] = dla.y; d.dl[2] = dla.z; d.dl[3] = dla.w;
+            d.dl[4] = dlb.x; d.dl[5] = dlb.y; d.dl[6] = dlb.z; d.dl[7] = dlb.w;
+            d.bt[0] = bta.x; d.bt[1] = bta.y; d.bt[2] = bta.z; d.bt[3] = bta.w;
+            d.bt[4] = btb.x; d.bt[5] = btb.y; d.bt[6] = btb.z; d.bt[7] = btb.w;
         }
     };
-    const auto stage_tile = [&]() {
+    const auto stage_tile = [&](const Pre& c) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
             const int cc = gtid + i * 256;
@@ -391,10 +410,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
                 half_t* rm = which ? Os : Qs;
                 half_t* tr = which ? Ot : Qt;
-                *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = sreg[i];
+                *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = c.s[i];
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    tr[(perm_base8(col, DP / 4) + perm_off8(j)) * T::kTLd + row] = sreg[i][j];
+                    tr[(perm_base8(col, DP / 4) + perm_off8(j)) * T::kTLd + row] = c.s[i][j];
             }
         }
     };
@@ -420,7 +439,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     float4v accv[T::kDB], acck[T::kDB];
 
     if (total > 0) {
-        fetch(n_begin, 0);
+        fetch(pre, n_begin, 0);
         fetch_kv(n_begin);
     }
     for (int t = 0, it = 0, n = n_begin; t < total; ++t) {
@@ -442,18 +461,19 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         }
 
         __syncthreads();  // this group's previous tile (and the last row's combine) are done
-        stage_tile();
-        // p = exp2(s scale log2e + bl), bl = (bias or the masked logit) log2e - lse2
+        stage_tile(pre);
+        // p = exp2(s scale log2e + bl), bl = (bias or the masked logit) log2e - lse2, formed
+        // here (pinned) so the next fetch may overwrite the prefetched values without copies
         float bl[8], dl[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            bl[j] = (kalive ? (float)bbn[j] : kMaskedLogit) * kLog2e - l2n[j];
-            dl[j] = dln[j];
+            bl[j] = pin_f32((kalive ? pre.bt[j] : kMaskedLogit * kLog2e) - pre.l2[j]);
+            dl[j] = pre.dl[j];
         }
         __syncthreads();
         if (t + 1 < total) {
             const bool wrap = it + 1 == IT;
-            fetch(wrap ? n + 1 : n, wrap ? 0 : it + 1);
+            fetch(pre, wrap ? n + 1 : n, wrap ? 0 : it + 1);
         }
 
         if (valid) {
@@ -576,6 +596,43 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
+// biast[h][key][q] = bias[h][q][key] * log2e for q < Sq, key < Sk, else 0, over [H][SkA][SqA]:
+// a workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads where the bias
+// rows allow them and 16-byte stores (SqA is a multiple of 32).
+__global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
+    __shared__ float tile[32][65];
+    const int qtiles = a.SqA / 32;
+    const int item = blockIdx.x;
+    const int qt = item % qtiles, rest = item / qtiles;
+    const int kblk = rest % a.kblocks, h = rest / a.kblocks;
+    const int tid = threadIdx.x;
+    const int q0 = qt * 32, k0 = kblk * 64;
+    {
+        const int qq = tid / 8, kc = (tid % 8) * 8;
+        const int gq = q0 + qq;
+        const int valid = gq < a.Sq ? a.Sk - (k0 + kc) : 0;
+        const half_t* src = a.bias + ((int64_t)h * a.Sq + (gq < a.Sq ? gq : 0)) * a.Sk + k0 + kc;
+        half8 b;
+        if (a.bias_vec && valid >= 8) {
+            b = bld8(src);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b[j] = j < valid ? src[j] : (half_t)0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[qq][kc + j] = (float)b[j] * kLog2e;
+    }
+    __syncthreads();
+    {
+        const int kk = tid / 4, qc = (tid % 4) * 8;
+        float* dst = a.biast + ((int64_t)h * a.SkA + k0 + kk) * a.SqA + q0 + qc;
+        *reinterpret_cast<float4*>(dst) =
+            make_float4(tile[qc][kk], tile[qc + 1][kk], tile[qc + 2][kk], tile[qc + 3][kk]);
+        *reinterpret_cast<float4*>(dst + 4) =
+            make_float4(tile[qc + 4][kk], tile[qc + 5][kk], tile[qc + 6][kk], tile[qc + 7][kk]);
+    }
+}
+
 // dbias[h][q][64 kblk + kk] = sum over chunks, in chunk order, of partial[c][h][kblk][kk][q]
 __global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(BwdArgs a) {
     __shared__ float tile[64][65];
@@ -647,7 +704,8 @@ struct BwdPlan {
     int QG = 1;  // query groups of the dK/dV kernel
     int SqP = 0, kblocks = 0, chunk = 0, chunks = 0;
     size_t stage_lds = 0, dbias_lds = 0;
-    size_t delta_bytes = 0, partial_bytes = 0;
+    int SqA = 0, SkA = 0;
+    size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0;
     std::string error;
 };
 
@@ -693,10 +751,11 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     int per_cu = std::max(1, std::min(2048 / threads, limit > 0 ? (int)(limit / per_wg) : 1));
     const int64_t slots = (int64_t)cu_count(device) * per_cu;
     const int64_t cols = std::max<int64_t>(H * p.kblocks, 1);
+    const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
     int64_t best = 1, best_cost = INT64_MAX;
-    for (int64_t ch = 1; ch <= std::max<int64_t>(N, 1); ++ch) {
-        const int64_t rows = (N + ch - 1) / ch;
-        const int64_t real = (N + rows - 1) / rows;
+    for (int64_t ch = 1; ch <= Nr; ++ch) {
+        const int64_t rows = (Nr + ch - 1) / ch;
+        const int64_t real = (Nr + rows - 1) / rows;
         const int64_t rounds = (real * cols + slots - 1) / slots;
         // each extra chunk adds a dbias partial to write and sum; a row costs about 24 of them
         const int64_t cost = rounds * rows * 24 + real;
@@ -705,10 +764,12 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
             best = real;
         }
     }
-    p.chunk = (int)((N + best - 1) / best);
-    if (p.chunk <= 0) p.chunk = 1;
+    p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
-    p.delta_bytes = round256((size_t)N * H * Sq * sizeof(float));
+    p.SqA = (int)(((Sq + 31) / 32) * 32);
+    p.SkA = p.kblocks * 64;
+    p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // delta, and lse2 after it
+    p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(float));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * 64 * p.SqP * sizeof(float));
     return p;
 }
@@ -740,6 +801,8 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     const int64_t g1 = qt * a.H * a.N;
     if (g1 > INT32_MAX) return invalid("attention_bwd: too many work items");
     stage_mark(stream, 0);
+    const int64_t gb = (int64_t)(a.SqA / 32) * p.kblocks * a.H;
+    hipLaunchKernelGGL(attn_bwd_biast_kernel, dim3((unsigned)gb), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
     stage_mark(stream, 1);
     if (p.QG == 4) {
@@ -773,7 +836,7 @@ extern "C" size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buf
                                                    const clk_buffer* k) {
     if (q == nullptr || k == nullptr || q->rank != 4 || k->rank != 4) return 0;
     const BwdPlan p = plan_bwd(device, q->dims[0], q->dims[1], q->dims[2], k->dims[2], q->dims[3]);
-    return p.delta_bytes + p.partial_bytes;
+    return 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes;
 }
 
 extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q,
@@ -812,8 +875,8 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     }
     const BwdPlan p = plan_bwd(device, N, H, Sq, Sk, D);
     if (want_dbias && !p.error.empty()) return invalid(p.error);
-    if (N * H * Sq == 0 && H * Sq * Sk == 0) return ok();
-    const size_t need = p.delta_bytes + p.partial_bytes;
+    if (N * H * Sq == 0 && N * H * Sk == 0 && H * Sq * Sk == 0) return ok();  // nothing to write
+    const size_t need = 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes;
     if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u)) {
         return fail(CLK_INTERNAL, "volta_mma_bwd: the workspace must be 256-byte aligned and hold " +
                                       std::to_string(need) + " bytes");
@@ -831,10 +894,15 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.dk = static_cast<half_t*>(dk->data);
     a.dv = static_cast<half_t*>(dv->data);
     a.dbias = static_cast<float*>(dbias->data);
-    a.delta = static_cast<float*>(workspace);
-    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.delta_bytes);
+    char* ws = static_cast<char*>(workspace);
+    a.delta = reinterpret_cast<float*>(ws);
+    a.lse2p = reinterpret_cast<float*>(ws + p.delta_bytes);
+    a.biast = reinterpret_cast<float*>(ws + 2 * p.delta_bytes);
+    a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
     a.SqP = p.SqP;
+    a.SqA = p.SqA;
+    a.SkA = p.SkA;
     a.kblocks = p.kblocks;
     a.chunk = p.chunk;
     a.chunks = p.chunks;
@@ -843,12 +911,15 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (N * H * Sq == 0 || Sk == 0) {
-        // nothing to differentiate: zero gradients (dk, dv keep their shape with Sk == 0)
-        const int64_t nq = N * H * Sq * D;
-        if (nq > 0) {
-            hipLaunchKernelGGL(fill_zero_f32, dim3(256), dim3(256), 0, s,
-                               static_cast<float*>(dq->data), nq / 2);
+        // no query or no key: every gradient is an empty sum (fp16 tensors have an even element
+        // count since D is even)
+        const int64_t nq = N * H * Sq * D, nk = N * H * Sk * D, nb = H * Sq * Sk;
+        if (nq > 0) hipLaunchKernelGGL(fill_zero_f32, dim3(256), dim3(256), 0, s, static_cast<float*>(dq->data), nq / 2);
+        if (nk > 0) {
+            hipLaunchKernelGGL(fill_zero_f32, dim3(256), dim3(256), 0, s, static_cast<float*>(dk->data), nk / 2);
+            hipLaunchKernelGGL(fill_zero_f32, dim3(256), dim3(256), 0, s, static_cast<float*>(dv->data), nk / 2);
         }
+        if (nb > 0) hipLaunchKernelGGL(fill_zero_f32, dim3(256), dim3(256), 0, s, a.dbias, nb);
         return launch_status("attention_bwd");
     }
     if (p.DP == 32) return launch_bwd<32>(s, a, p, want_dbias);

@@ -153,3 +153,20 @@ def test_want_flags(hip):
     for name, x, y in zip(("dq", "dk", "dv"), on[:3], off[:3]):
         assert np.array_equal(x, y), name + " changed when want_dbias was off"
     assert np.abs(off[3]).max() == 0.0, "dbias was written although want_dbias was off"
+
+
+@pytest.mark.parametrize("n,sq,sk", [(2, 0, 40), (0, 24, 40), (2, 24, 0)])
+def test_empty_problems(hip, n, sq, sk):
+    """No query, no row or no key: every gradient is an empty sum, written as zeros over the
+    NaN the results held before the call."""
+    h, d = 2, 32
+    q = torch.zeros((n, h, sq, d), dtype=torch.float16, device="cuda")
+    k = torch.zeros((n, h, sk, d), dtype=torch.float16, device="cuda")
+    bias = torch.zeros((h, sq, sk), dtype=torch.float16, device="cuda")
+    kmask = torch.ones((n, sk), dtype=torch.uint8, device="cuda")
+    lse = torch.zeros((n, h, sq), dtype=torch.float32, device="cuda")
+    grads = (torch.full_like(q, float("nan")), torch.full_like(k, float("nan")),
+             torch.full_like(k, float("nan")), torch.full(bias.shape, float("nan"), device="cuda"))
+    hip.attention_bwd(q, k, k, bias, kmask, q, q, lse, d ** -0.5, grads=grads)
+    for name, t in zip(("dq", "dk", "dv", "dbias"), host(*grads)):
+        assert t.size == 0 or np.abs(t).max() == 0.0, name
