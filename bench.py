@@ -1,24 +1,32 @@
 #!/usr/bin/env python3
 """Benchmark of the ColabFold legacy-kernel hot path on one MI355X (gfx950).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused] [--no-packed]
+                  [--calibration-copy MIB]
+  python bench.py --stats-summary DIR            (text summary of a rocprofv3 --stats run)
+  python bench.py --traffic-summary FETCH_DIR WRITE_DIR [--calibration-copy MIB]
+                                                 (HBM bytes per dispatch from two --pmc runs)
 
 A step is one attention forward + backward of BASELINE config C3 (MSA row attention with pair
 bias, fp16: N_seq = 512 rows, N_res = 384, H = 8, D = 32): VoltaMma(want_lse) then
 VoltaMmaBwd(want_dbias), through the library's C ABI on the current stream, inputs already in
-HBM. value is the step's algorithmic TFLOP/s (14 u flops, u = N H S^2 D, as BASELINE counts
-it: the backward's recompute of S included). Per-kernel durations come from HIP events the
-library records at its kernel boundaries during the timed steps (clk_set_stage_events); the
-roofline object is the dominant kernel's. The fused LayerNorm projections (config C4,
-M = 262144 rows, c = 64 and 128) are timed separately, rotating enough buffer sets that no call
-finds its inputs in the 256 MB Infinity Cache, and reported under "fused". cpu_baseline is the
-fp32 torch-CPU restatement of the reference tests' jnp attention (oracle/cpu_ref.py; jax is not
-installed) on a bounded row sample of the same workload, on this box's host cores.
+HBM. value is the step's algorithmic TFLOP/s (14 u flops, u = N H S^2 D: forward 4u, backward
+10u with its recompute of S). Per-kernel durations come from HIP events that the library records
+on its launch stream at its kernel boundaries (clk_set_stage_events); the roofline object is the
+dominant kernel's, its "traffic" the HBM bytes per dispatch that the committed rocprofv3 counter
+summary (profiles/attention_c3_traffic.txt) measured for that kernel. Reported beside the step:
+the gated packed forward VoltaMmaPacked (G = 4) on the same shape, and the fused pair-stack ops
+of config C4 (M = 262144 rows, c = 64 and 128), each timed over enough rotating buffer sets that
+no call finds its inputs in the 256 MB Infinity Cache. cpu_baseline is the fp32 torch-CPU
+restatement of the reference tests' jnp attention (oracle/cpu_ref.py; jax is not installed) on a
+bounded row sample of the same workload, on this box's host cores.
 
 One GPU per box here: --gpus above 1 exits with a message.
 """
 import argparse
+import csv
 import ctypes
+import glob
 import json
 import math
 import os
@@ -34,8 +42,16 @@ METRIC = "ms/call + TFLOP/s attn fwd+bwd (N_res=384); fused LN-proj GB/s, 1 GPU"
 PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
 PEAK_GBS = 8000.0      # MI355X HBM3E
 MALL_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_c3_traffic.txt")
 
 N, H, S, D = 512, 8, 384, 32
+FWD_STAGES = ("attn_fwd",)
+BWD_STAGES = ("bwd_biast", "bwd_dq", "bwd_dkdv", "bwd_dbias")
+# kernel-name fragment in a rocprofv3 record -> the bench's stage name
+KERNEL_STAGES = (("attn_fwd_kernel", "attn_fwd"), ("attn_bwd_biast_kernel", "bwd_biast"),
+                 ("attn_bwd_dq_kernel", "bwd_dq"), ("attn_bwd_dkdv_kernel", "bwd_dkdv"),
+                 ("attn_bwd_dbias_kernel", "bwd_dbias"))
+CALIBRATION_KERNEL = "bitwise_not"
 
 
 class HipEvents:
@@ -78,13 +94,38 @@ def disarm(hip):
     hip.lib().clk_set_stage_events(None, 0)
 
 
-def attention_bytes():
-    """Algorithmic HBM bytes per launch (each tensor read or written once)."""
-    t = N * H * S * D * 2          # one fp16 [N,H,S,D] tensor
-    row = N * H * S * 4            # one fp32 [N,H,S] row statistic
-    bias = H * S * S * 2
-    km = N * S
-    return t, row, bias, km
+def roof_entry(ms_list, flops, byts, **extra):
+    """Per-kernel timing against both roofs; the bound is the larger ideal time."""
+    mean, med = statistics.mean(ms_list), statistics.median(ms_list)
+    t_mfma = flops / (PEAK_TFLOPS * 1e12) * 1e3
+    t_hbm = byts / (PEAK_GBS * 1e9) * 1e3
+    e = {"ms": round(mean, 5), "ms_median": round(med, 5), "calls": len(ms_list),
+         "tflops": round(flops / mean / 1e9, 2), "gbs": round(byts / mean / 1e6, 1),
+         "bound": "mfma" if t_mfma > t_hbm else "hbm",
+         "frac": round(max(t_mfma, t_hbm) / mean, 4), "frac_mfma": round(t_mfma / mean, 4),
+         "frac_hbm": round(t_hbm / mean, 4), "algo_flops": flops, "algo_bytes": byts}
+    e.update(extra)
+    return e
+
+
+def attention_algo(ws_bytes):
+    """(flops, bytes) per launch of each C3 kernel. Bytes count every tensor of the kernel's
+    contract read or written once; implementation scratch is listed apart (scratch_bytes)."""
+    u = float(N) * H * S * S * D
+    t = N * H * S * D * 2                   # one fp16 [N,H,S,D] tensor
+    row = N * H * S * 4                     # one fp32 [N,H,S] row statistic
+    bias, km, dbias = H * S * S * 2, N * S, H * S * S * 4
+    sqa, ska = -(-S // 32) * 32, -(-S // 64) * 64
+    biast = H * ska * sqa * 4
+    partial = max(ws_bytes - 2 * row - biast, 0)
+    return {
+        "attn_fwd": (4 * u, 3 * t + bias + km + t + row, 0),
+        "bwd_biast": (0.0, bias + biast, 0),
+        # dQ = dS K is 2u; the kernel also recomputes S and dP (4u more)
+        "bwd_dq": (2 * u, 5 * t + row + bias + km + t, 2 * row),
+        "bwd_dkdv": (8 * u, 4 * t + row + bias + km + 2 * t, partial),
+        "bwd_dbias": (0.0, dbias, partial),
+    }
 
 
 def bench_attention(torch, hip, steps, warmup, ev):
@@ -100,25 +141,26 @@ def bench_attention(torch, hip, steps, warmup, ev):
         out = torch.empty_like(q)
         lse = torch.empty((N, H, S), dtype=torch.float32, device="cuda")
         ws = torch.empty(hip.attention_bwd_workspace(q, k), dtype=torch.uint8, device="cuda")
-        sets.append((q, k, v, bias, kmask, dout, out, lse, ws))
+        grads = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+                 torch.empty((H, S, S), dtype=torch.float32, device="cuda"))
+        sets.append((q, k, v, bias, kmask, dout, out, lse, ws, grads))
 
     def step(st, fwd_ev=None, bwd_ev=None):
-        q, k, v, bias, kmask, dout, out, lse, ws = st
+        q, k, v, bias, kmask, dout, out, lse, ws, grads = st
         if fwd_ev:
             arm(hip, fwd_ev)
         hip.attention_fwd(q, k, v, bias, kmask, scale, 64, 32, True, out=out, lse=lse)
         if bwd_ev:
             arm(hip, bwd_ev)
-        r = hip.attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, True, workspace=ws)
+        hip.attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, True, workspace=ws, grads=grads)
         if bwd_ev:
             disarm(hip)
-        return r
 
     for i in range(warmup):
         step(sets[i % 2])
     torch.cuda.synchronize()
-    fwd_evs = [ev.create(2) for _ in range(steps)]
-    bwd_evs = [ev.create(4) for _ in range(steps)]
+    fwd_evs = [ev.create(len(FWD_STAGES) + 1) for _ in range(steps)]
+    bwd_evs = [ev.create(len(BWD_STAGES) + 1) for _ in range(steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -127,45 +169,74 @@ def bench_attention(torch, hip, steps, warmup, ev):
     stop.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(stop)
-    per = {"attn_fwd": [], "bwd_dq": [], "bwd_dkdv": [], "bwd_dbias": []}
+    per = {name: [] for name in FWD_STAGES + BWD_STAGES}
     for fe, be in zip(fwd_evs, bwd_evs):
-        per["attn_fwd"].append(ev.elapsed_ms(fe[0], fe[1]))
-        per["bwd_dq"].append(ev.elapsed_ms(be[0], be[1]))
-        per["bwd_dkdv"].append(ev.elapsed_ms(be[1], be[2]))
-        per["bwd_dbias"].append(ev.elapsed_ms(be[2], be[3]))
+        for i, name in enumerate(FWD_STAGES):
+            per[name].append(ev.elapsed_ms(fe[i], fe[i + 1]))
+        for i, name in enumerate(BWD_STAGES):
+            per[name].append(ev.elapsed_ms(be[i], be[i + 1]))
     for e in fwd_evs + bwd_evs:
         ev.destroy(e)
     disarm(hip)
 
-    t, row, bias_b, km = attention_bytes()
-    ws_bytes = sets[0][8].numel()
-    partial = max(ws_bytes - row, 0)
-    algo = {  # (flops, bytes) per launch
-        "attn_fwd": (4 * u, 3 * t + bias_b + km + t + row),
-        "bwd_dq": (6 * u, 5 * t + row + bias_b + km + t + row),
-        "bwd_dkdv": (8 * u, 4 * t + 2 * row + bias_b + km + 2 * t + partial),
-        "bwd_dbias": (0.0, partial + H * S * S * 4),
-    }
-    kernels = {}
-    for name, ds in per.items():
-        ms = statistics.mean(ds)
-        fl, by = algo[name]
-        t_mfma = fl / (PEAK_TFLOPS * 1e12) * 1e3
-        t_hbm = by / (PEAK_GBS * 1e9) * 1e3
-        kernels[name] = {"ms": round(ms, 5), "tflops": round(fl / ms / 1e9, 2),
-                         "gbs": round(by / ms / 1e6, 1), "bound": "mfma" if t_mfma > t_hbm else "hbm",
-                         "frac_mfma": round(t_mfma / ms, 4), "frac_hbm": round(t_hbm / ms, 4),
-                         "algo_flops": fl, "algo_bytes": by}
-    ms_step = total_ms / steps
-    return ms_step, 14 * u, kernels
+    algo = attention_algo(sets[0][8].numel())
+    kernels = {name: roof_entry(per[name], algo[name][0], algo[name][1], scratch_bytes=algo[name][2])
+               for name in per}
+    return total_ms / steps, 14 * u, kernels
 
 
-def fused_cases(torch):
-    """(name, c, callable factory) for the C4 fused ops at M = 262144 rows."""
-    return [("ln_projection", 64), ("ln_projection", 128), ("output_projection", 64),
-            ("output_projection", 128), ("ln_gdp", 64), ("ln_gdp", 128),
-            ("trimul_epilogue", 64), ("trimul_epilogue", 128), ("transition", 64),
-            ("transition", 128)]
+def bench_packed(torch, hip, iters, warmup, ev):
+    """VoltaMmaPacked (G = 4: q, k, v and the gate in one [X, Y, 4, H, D] tensor) on C3's shape."""
+    u = float(N) * H * S * S * D
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2)
+    sets = []
+    for _ in range(2):
+        p = torch.randn((N, S, 4, H, D), generator=g, device="cuda").half()
+        bias = torch.randn((H, S, S), generator=g, device="cuda").half()
+        kmask = torch.ones((N, S), dtype=torch.uint8, device="cuda")
+        gate_bias = torch.zeros(H * D, dtype=torch.float16, device="cuda")
+        out = torch.empty((N, S, H, D), dtype=torch.float16, device="cuda")
+        sets.append((p, bias, kmask, gate_bias, out))
+    for i in range(warmup):
+        p, bias, kmask, gb, out = sets[i % 2]
+        hip.attention_packed(p, bias, kmask, gb, D ** -0.5, out=out)
+    torch.cuda.synchronize()
+    evs = [ev.create(2) for _ in range(iters)]
+    for i in range(iters):
+        p, bias, kmask, gb, out = sets[i % 2]
+        arm(hip, evs[i])
+        hip.attention_packed(p, bias, kmask, gb, D ** -0.5, out=out)
+    disarm(hip)
+    torch.cuda.synchronize()
+    ms = [ev.elapsed_ms(e[0], e[1]) for e in evs]
+    for e in evs:
+        ev.destroy(e)
+    t = N * H * S * D * 2
+    return roof_entry(ms, 4 * u, 4 * t + H * S * S * 2 + N * S + t + H * D * 2)
+
+
+def fused_bytes_flops(op, m, c, n=None, heads=0):
+    """Algorithmic HBM bytes (activations read and results written once, weights excluded) and
+    flops per call of a fused op at width c over m rows."""
+    if op == "ln_gdp":
+        p = 2 * c
+        return float(m * c * 2 + m * 2 + m * p * 2), 2.0 * m * c * (2 * p)
+    if op == "trimul_epilogue":
+        return float(m * c * 4 + m * c * 2 + m * c * 2), 2.0 * m * c * c * 2
+    if op == "ln_projection":
+        return float(m * c * 2 + m * n * 2 + m * heads * 2), 2.0 * m * c * (n + heads)
+    if op == "output_projection":
+        return float(m * n * 2 + m * c * 2 * 2), 2.0 * m * n * c   # o and residual read, out written
+    if op == "transition":
+        return float(m * c * 2 * 2), 2.0 * m * c * (4 * c) * 2
+    raise KeyError(op)
+
+
+FUSED_CASES = (("ln_projection", 64), ("ln_projection", 128), ("output_projection", 64),
+               ("output_projection", 128), ("ln_gdp", 64), ("ln_gdp", 128),
+               ("trimul_epilogue", 64), ("trimul_epilogue", 128), ("transition", 64),
+               ("transition", 128))
 
 
 def make_fused(torch, hip, op, c, M, g):
@@ -179,58 +250,40 @@ def make_fused(torch, hip, op, c, M, g):
     if op == "ln_projection":
         x, sc, of = h(M, c), f(c, s=.1, mean=1.), f(c, s=.1)
         wT, wbT = h(512, c, s=c ** -.5), h(4, c, s=c ** -.5)
-        p = torch.empty((M, 512), dtype=torch.float16, device="cuda")
-        bias = torch.empty((4, M), dtype=torch.float16, device="cuda")
-        one = torch.zeros(1, dtype=torch.float16, device="cuda")
-        bufs = [hip.buffer(t) for t in (x, sc, of, wT, wbT, one, p, bias)]
-        keepalive = (x, sc, of, wT, wbT, one, p, bias)
-        return lambda: hip._check(hip.lib().clk_ln_projection(hip._stream(x), *map(hip._ref, bufs), 1e-5, 512, 4, 0)), keepalive
+        return lambda: hip.ln_projection(x, sc, of, wT, wbT), (x, wT, wbT)
     if op == "output_projection":
         o, wT, b, r = h(M, 128), h(c, 128, s=128 ** -.5), h(c, s=.1), h(M, c)
-        one = torch.zeros(1, dtype=torch.float16, device="cuda")
         out = torch.empty((M, c), dtype=torch.float16, device="cuda")
-        bufs = [hip.buffer(t) for t in (o, wT, b, r, one, out)]
-        return lambda: hip._check(hip.lib().clk_output_projection(hip._stream(o), *map(hip._ref, bufs), 1, 0)), (o, wT, b, r, one, out)
+        return lambda: hip.output_projection(o, wT, b, residual=r, out=out), (o, r, out)
     if op == "ln_gdp":
         x, sc, of = h(M, c), f(c, s=.1, mean=1.), f(c, s=.1)
         wpT, wgT, bp, bg = h(2 * c, c, s=c ** -.5), h(2 * c, c, s=c ** -.5), h(2 * c, s=.1), h(2 * c, s=.1)
         mask = torch.ones(M, dtype=torch.float16, device="cuda")
-        left = torch.empty((c, M), dtype=torch.float16, device="cuda")
-        right = torch.empty((c, M), dtype=torch.float16, device="cuda")
-        bufs = [hip.buffer(t) for t in (x, sc, of, wpT, bp, wgT, bg, mask, left, right)]
-        return lambda: hip._check(hip.lib().clk_ln_gdp(hip._stream(x), *map(hip._ref, bufs), 1e-5)), (x, sc, of, wpT, bp, wgT, bg, mask, left, right)
+        return lambda: hip.ln_gdp(x, sc, of, wpT, bp, wgT, bg, mask), (x, mask)
     if op == "trimul_epilogue":
         x_cm, x = f(c, M), h(M, c)
         ins, ino, lns, lno = f(c, s=.1, mean=1.), f(c, s=.1), f(c, s=.1, mean=1.), f(c, s=.1)
         woT, bo, wgT, bg = h(c, c, s=c ** -.5), h(c, s=.1), h(c, c, s=c ** -.5), h(c, s=.1)
-        one = torch.zeros(1, dtype=torch.float16, device="cuda")
         out = torch.empty((M, c), dtype=torch.float16, device="cuda")
-        bufs = [hip.buffer(t) for t in (x_cm, x, ins, ino, lns, lno, woT, bo, wgT, bg, one, out)]
-        return lambda: hip._check(hip.lib().clk_trimul_epilogue(hip._stream(x), *map(hip._ref, bufs), 1e-5, 0, 0)), (x_cm, x, ins, ino, lns, lno, woT, bo, wgT, bg, one, out)
+        return (lambda: hip.trimul_epilogue(x_cm, x, ins, ino, lns, lno, woT, bo, wgT, bg, out=out),
+                (x_cm, x, out))
     if op == "transition":
         hd = 4 * c
         x, sc, of = h(M, c), f(c, s=.1, mean=1.), f(c, s=.1)
         w1T, b1, w2T, b2 = h(hd, c, s=c ** -.5), h(hd, s=.1), h(hd // 64, c, 64, s=hd ** -.5), h(c, s=.1)
-        one = torch.zeros(1, dtype=torch.float16, device="cuda")
         out = torch.empty((M, c), dtype=torch.float16, device="cuda")
-        bufs = [hip.buffer(t) for t in (x, sc, of, w1T, b1, w2T, b2, one, out)]
-        return lambda: hip._check(hip.lib().clk_transition(hip._stream(x), *map(hip._ref, bufs), 1e-5, 0, 0)), (x, sc, of, w1T, b1, w2T, b2, one, out)
+        return lambda: hip.transition(x, sc, of, w1T, b1, w2T, b2, out=out), (x, out)
     raise KeyError(op)
 
 
-def bench_fused(torch, hip, ev, iters=20, warmup=3):
-    from oracle import fused as orf
+def bench_fused(torch, hip, ev, iters, warmup):
     M = 262144
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
     res = {}
-    for op, c in fused_cases(torch):
-        if op == "ln_projection":
-            byts, flops = orf.fused_bytes_flops(op, M, c, n=512, heads=4)
-        elif op == "output_projection":
-            byts, flops = orf.fused_bytes_flops(op, M, c, n=128)
-        else:
-            byts, flops = orf.fused_bytes_flops(op, M, c)
+    for op, c in FUSED_CASES:
+        byts, flops = fused_bytes_flops(op, M, c, n=512 if op == "ln_projection" else 128,
+                                        heads=4 if op == "ln_projection" else 0)
         nsets = max(3, math.ceil(3 * MALL_BYTES / byts))
         calls = [make_fused(torch, hip, op, c, M, g) for _ in range(nsets)]
         for i in range(warmup):
@@ -242,16 +295,10 @@ def bench_fused(torch, hip, ev, iters=20, warmup=3):
             calls[i % nsets][0]()
         disarm(hip)
         torch.cuda.synchronize()
-        ms = statistics.median(ev.elapsed_ms(e[0], e[1]) for e in evs)
+        ms = [ev.elapsed_ms(e[0], e[1]) for e in evs]
         for e in evs:
             ev.destroy(e)
-        t_hbm = byts / (PEAK_GBS * 1e9) * 1e3
-        t_mfma = flops / (PEAK_TFLOPS * 1e12) * 1e3
-        bound = "mfma" if t_mfma > t_hbm else "hbm"
-        res["%s_c%d" % (op, c)] = {
-            "ms": round(ms, 5), "gbs": round(byts / ms / 1e6, 1), "tflops": round(flops / ms / 1e9, 2),
-            "bound": bound, "frac": round(max(t_hbm, t_mfma) / ms, 4), "frac_hbm": round(t_hbm / ms, 4),
-            "algo_bytes": byts, "algo_flops": flops, "buffer_sets": nsets}
+        res["%s_c%d" % (op, c)] = roof_entry(ms, flops, byts, buffer_sets=nsets)
         del calls
         torch.cuda.empty_cache()
     return res
@@ -260,7 +307,7 @@ def bench_fused(torch, hip, ev, iters=20, warmup=3):
 def cpu_baseline(torch):
     """The fp32 torch-CPU attention fwd+bwd on a row sample of C3, as TFLOP/s."""
     from oracle import cpu_ref
-    rows = 32
+    rows = 128
     g = torch.Generator()
     g.manual_seed(0)
     q, k, v, dout = (torch.randn((rows, H, S, D), generator=g).half().float() for _ in range(4))
@@ -277,21 +324,123 @@ def cpu_baseline(torch):
     flops = 14.0 * rows * H * S * S * D
     return {"value": round(flops / sec / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": "%d of the 512 C3 rows, fwd+bwd by autograd, fp32, median of 5 after 1 warm-up "
-                      "(%.3f s per sample; whole C3 step would take %.1f s)" % (rows, sec, sec * N / rows)}
+            "sample": "%d of the 512 C3 rows, fwd+bwd by autograd, fp32 torch-CPU, median of 5 after 1 "
+                      "warm-up (%.3f s per sample; the whole C3 step would take %.1f s)"
+                      % (rows, sec, sec * N / rows)}
+
+
+def calibration_copy(torch, mib):
+    """A plain streaming kernel of known size for the HBM byte counters: bitwise_not over an
+    int16 tensor of `mib` MiB reads and writes exactly that many bytes (3 calls)."""
+    src = torch.ones(mib << 19, dtype=torch.int16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+
+
+# ---- rocprofv3 summaries -----------------------------------------------------------------
+
+def _stage_of(kernel_name):
+    for frag, stage in KERNEL_STAGES:
+        if frag in kernel_name:
+            return stage
+    return None
+
+
+def stats_summary(d):
+    """Text table of every *kernel_stats.csv under d (rocprofv3 --kernel-trace --stats)."""
+    files = sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True))
+    if not files:
+        raise SystemExit("no kernel_stats.csv under " + d)
+    lines = ["%-64s %7s %12s %12s %12s %7s" % ("kernel", "calls", "avg_us", "min_us", "max_us", "pct")]
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            name = r["Name"].replace("void ", "")
+            name = name if len(name) <= 64 else name[:61] + "..."
+            lines.append("%-64s %7s %12.2f %12.2f %12.2f %7.2f" % (
+                name, r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3,
+                float(r["MaxNs"]) / 1e3, float(r["Percentage"])))
+    return "\n".join(lines)
+
+
+def _counter_means(d, counter):
+    """Mean per dispatch of `counter` (summed over its instances) for each kernel name."""
+    per = {}
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit("no counter_collection.csv under " + d)
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    out = {}
+    for (name, _), v in per.items():
+        out.setdefault(name, []).append(v)
+    return {name: statistics.mean(v) for name, v in out.items()}
+
+
+def traffic_summary(fetch_dir, write_dir, mib):
+    """HBM bytes per dispatch: FETCH_SIZE and WRITE_SIZE (KiB) scaled by what the same counters
+    read for the calibration copy of known size."""
+    fetch, write = _counter_means(fetch_dir, "FETCH_SIZE"), _counter_means(write_dir, "WRITE_SIZE")
+    cal = [n for n in fetch if CALIBRATION_KERNEL in n]
+    if not cal or not any(CALIBRATION_KERNEL in n for n in write):
+        raise SystemExit("the runs hold no calibration copy (--calibration-copy)")
+    known_kib = float(mib) * 1024
+    f_fetch = known_kib / fetch[cal[0]]
+    f_write = known_kib / next(write[n] for n in write if CALIBRATION_KERNEL in n)
+    lines = ["calibration: %s over %d MiB reads FETCH_SIZE %.0f KiB and writes WRITE_SIZE %.0f KiB "
+             "per dispatch; scale factors fetch %.4f, write %.4f"
+             % (CALIBRATION_KERNEL, mib, fetch[cal[0]], known_kib / f_write, f_fetch, f_write)]
+    seen = {}
+    for name in sorted(fetch):
+        stage = _stage_of(name)
+        if stage is None or name not in write:
+            continue
+        by = (fetch[name] * f_fetch + write[name] * f_write) * 1024
+        seen[stage] = by
+        lines.append("kernel %s fetch_kib %.0f write_kib %.0f traffic_bytes %.0f  (%s)"
+                     % (stage, fetch[name], write[name], by, name.replace("void ", "")[:60]))
+    return "\n".join(lines)
+
+
+def load_traffic(stage):
+    """HBM bytes per dispatch of `stage` from the committed counter summary, or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            t = line.split()
+            if len(t) >= 8 and t[0] == "kernel" and t[1] == stage and t[6] == "traffic_bytes":
+                return float(t[7])
+    except OSError:
+        return None
+    return None
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
+    ap.add_argument("--no-packed", action="store_true")
+    ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB")
+    ap.add_argument("--stats-summary", metavar="DIR")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary))
+        return
+    if args.traffic_summary:
+        print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.calibration_copy or 256))
+        return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU per box; --gpus %d is not supported "
-              "(the path shards by batch rows; see the design notes)" % args.gpus, file=sys.stderr)
+              "(the path shards by batch rows across GPUs, which no run here exercises)" % args.gpus,
+              file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -300,17 +449,19 @@ def main():
     from colabfold_legacy_kernels import hip
     hip.lib()
     ev = HipEvents()
+    if args.calibration_copy:
+        calibration_copy(torch, args.calibration_copy)
     ms_step, flops_step, kernels = bench_attention(torch, hip, args.steps, args.warmup, ev)
     dom = max(kernels, key=lambda k: kernels[k]["ms"])
     kd = kernels[dom]
     if kd["bound"] == "mfma":
-        roof = {"bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(kd["tflops"] / PEAK_TFLOPS, 4)}
+        roof = {"bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_TFLOPS, "unit": "TFLOP/s"}
     else:
-        roof = {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(kd["gbs"] / PEAK_GBS, 4)}
+        roof = {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = load_traffic(dom)
     roof["kernel"] = dom
-    roof["traffic"] = None
+    roof["ms"] = kd["ms"]
     line = {
         "metric": METRIC,
         "value": round(flops_step / ms_step / 1e9, 2),
@@ -330,8 +481,10 @@ def main():
         "roofline": roof,
         "kernels": kernels,
     }
+    if not args.no_packed:
+        line["packed_fwd"] = bench_packed(torch, hip, args.steps, args.warmup, ev)
     if not args.no_fused:
-        line["fused"] = bench_fused(torch, hip, ev)
+        line["fused"] = bench_fused(torch, hip, ev, args.steps, args.warmup)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(line), flush=True)

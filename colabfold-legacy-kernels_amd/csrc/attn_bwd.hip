@@ -803,8 +803,9 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     stage_mark(stream, 0);
     const int64_t gb = (int64_t)(a.SqA / 32) * p.kblocks * a.H;
     hipLaunchKernelGGL(attn_bwd_biast_kernel, dim3((unsigned)gb), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
     stage_mark(stream, 1);
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
+    stage_mark(stream, 2);
     if (p.QG == 4) {
         if constexpr (DP == 32) launch_dkdv<DP, 4>(stream, a, p, want_dbias);
     } else if (p.QG == 2) {
@@ -812,7 +813,7 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     } else {
         launch_dkdv<DP, 1>(stream, a, p, want_dbias);
     }
-    stage_mark(stream, 2);
+    stage_mark(stream, 3);
     if (want_dbias) {
         const int64_t g3 = (int64_t)((a.Sq + 63) / 64) * p.kblocks * a.H;
         hipLaunchKernelGGL(attn_bwd_dbias_kernel, dim3((unsigned)g3), dim3(256), 0, stream, a);
@@ -820,7 +821,7 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
         const int64_t nb = (int64_t)a.H * a.Sq * a.Sk;
         hipLaunchKernelGGL(fill_zero_f32, dim3(1024), dim3(256), 0, stream, a.dbias, nb);
     }
-    stage_mark(stream, 3);
+    stage_mark(stream, 4);
     return launch_status("attention_bwd");
 }
 
