@@ -395,15 +395,15 @@ def traffic_summary(fetch_dir, write_dir, mib):
     lines = ["calibration: %s over %d MiB reads FETCH_SIZE %.0f KiB and writes WRITE_SIZE %.0f KiB "
              "per dispatch; scale factors fetch %.4f, write %.4f"
              % (CALIBRATION_KERNEL, mib, fetch[cal[0]], known_kib / f_write, f_fetch, f_write)]
-    seen = {}
     for name in sorted(fetch):
-        stage = _stage_of(name)
-        if stage is None or name not in write:
+        if "clk::" not in name or name not in write:
             continue
+        stage = _stage_of(name)
+        short = name.replace("void ", "").replace("clk::", "").split("(")[0].replace(" ", "")
         by = (fetch[name] * f_fetch + write[name] * f_write) * 1024
-        seen[stage] = by
-        lines.append("kernel %s fetch_kib %.0f write_kib %.0f traffic_bytes %.0f  (%s)"
-                     % (stage, fetch[name], write[name], by, name.replace("void ", "")[:60]))
+        lines.append("%s %s fetch_kib %.0f write_kib %.0f traffic_bytes %.0f"
+                     % ("kernel" if stage else "fused", stage or short, fetch[name], write[name], by)
+                     + ("  (%s)" % short if stage else ""))
     return "\n".join(lines)
 
 

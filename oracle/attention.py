@@ -173,8 +173,3 @@ def attention_packed(p, bias, kmask, gate_bias, column, scale=None, lims=None):
             o[np.asarray(lims[:-1]) == 0] = 0.0
     return repack_out(o, column)
 
-
-def attention_flops(n, h, sq, sk, d, backward=False):
-    """Algorithmic flops: 4u forward, 10u backward (with the S recompute), u = N H Sq Sk D."""
-    u = float(n) * h * sq * sk * d
-    return 10.0 * u if backward else 4.0 * u

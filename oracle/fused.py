@@ -171,28 +171,3 @@ def transition(x, scale, offset, w1T, b1, w2T, b2, keep, eps, add_input, round_m
     work = tile_work(keep, out.shape[0], rows, -1.0)
     return _apply_keep(out, work, rows, None if add_input else 0.0)
 
-
-def fused_bytes_flops(op, m, c, n=None, heads=0, hidden=None):
-    """Algorithmic HBM bytes (activations read + results written once, weights excluded) and
-    flops per call, for the bench's roofline."""
-    if op == 'ln_gdp':
-        p = 2 * c if n is None else n  # P = 2 ci with ci = c by default
-        byts = m * c * 2 + m * 2 + m * p * 2
-        flops = 2.0 * m * c * (2 * p)
-    elif op == 'trimul_epilogue':
-        byts = m * c * 4 + m * c * 2 + m * c * 2
-        flops = 2.0 * m * c * c * 2
-    elif op == 'ln_projection':
-        byts = m * c * 2 + m * n * 2 + m * heads * 2
-        flops = 2.0 * m * c * (n + heads)
-    elif op == 'output_projection':
-        k = c if n is None else n
-        byts = m * k * 2 + m * c * 2 * 2  # o read, residual read, out written
-        flops = 2.0 * m * k * c
-    elif op == 'transition':
-        hid = 4 * c if hidden is None else hidden
-        byts = m * c * 2 * 2
-        flops = 2.0 * m * c * hid * 2
-    else:
-        raise KeyError(op)
-    return float(byts), flops
