@@ -6,9 +6,10 @@ the same errors (KeyError for an unknown kernel, FileNotFoundError for a capabil
 file that is missing). The capability key is the gfx target number: 950, or the string
 "gfx950", which _resolve normalises to 950.
 
-symbol() names each kernel's reference XLA FFI target (VoltaMma, VoltaMmaBwd, VoltaLnProj, ...).
-The library's entry points are plain C functions, one per target (clk_attention_fwd, ...;
-include/colabfold_gfx950.h), which colabfold_legacy_kernels.hip calls from PyTorch.
+symbol() names each kernel's XLA FFI handler (VoltaMma, VoltaMmaBwd, VoltaLnProj, ...), which the
+library exports under the reference's names (include/colabfold_gfx950_xla.h). Under them is a
+plain C entry point per target (clk_attention_fwd, ...; include/colabfold_gfx950.h), which
+colabfold_legacy_kernels.hip calls from PyTorch.
 """
 
 from pathlib import Path

@@ -17,10 +17,10 @@
 //                 padded to whole 32-query tiles (0 and +inf past Sq).
 //   dkdv_kernel   one workgroup per (h, 64 keys, chunk of batch rows): for each row n of its
 //                 chunk it loops over query tiles, dV^T = dO^T P and dK^T = Q^T dS accumulate in
-//                 registers, and each wave adds its 16 keys' dS into an fp32 [64 keys][Sq] dBias
+//                 registers, and each wave adds its 16 keys' dS into an fp32 [Sq][64 keys] dBias
 //                 partial that stays in LDS for the whole chunk (one owner per element, fixed
 //                 order). The chunk's partial goes to the workspace once.
-//   dbias_kernel  dbias = the chunk partials summed in chunk order, transposed to [H,Sq,Sk].
+//   dbias_kernel  dbias = the chunk partials summed in chunk order.
 #include "clk_common.h"
 
 namespace clk {
@@ -41,10 +41,9 @@ struct BwdArgs {
     float* delta;    // workspace [N, H, SqA]: rowsum(out * dout), 0 past Sq
     float* lse2p;    // workspace [N, H, SqA]: lse, +inf past Sq
     float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside
-    float* partial;  // workspace [chunks][H][kblocks][64][SqP]
+    float* partial;  // workspace [chunks][H][kblocks][SqA][64]
     int N, H, Sq, Sk, D;
     int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
-    int SqP;         // partial row stride (floats)
     int kblocks;     // ceil(Sk / 64)
     int chunk;       // batch rows per dkdv workgroup
     int chunks;
@@ -326,6 +325,8 @@ struct DkdvTile {
     static constexpr int kStage = 2 * kBQ * kLd + 2 * DP * kTLd;   // halfs per query group
     static constexpr int kStageBytes = kStage * 2 * QG;
     static constexpr int kCombineBytes = 4 * (QG - 1) * kDB * kWave * 4 * 4;
+    // dBias partial [kBK keys][SqA + kDBPad]: the pad staggers the keys' rows across LDS banks
+    static constexpr int kDBPad = 4;
     static_assert(kCombineBytes <= kStageBytes, "the combine reuses the staging area");
 };
 
@@ -353,11 +354,12 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     half_t* Os = Qs + T::kBQ * T::kLd;
     half_t* Qt = Os + T::kBQ * T::kLd;
     half_t* Ot = Qt + DP * T::kTLd;
-    float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][SqP]
+    const int dbld = a.SqA + T::kDBPad;
+    float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][dbld]
     float* comb = reinterpret_cast<float*>(lds_raw);                   // between rows only
 
     if constexpr (DBIAS) {
-        for (int i = tid; i < T::kBK * a.SqP; i += T::kThreads) DBt[i] = 0.f;
+        for (int i = tid; i < T::kBK * dbld; i += T::kThreads) DBt[i] = 0.f;
     }
 
     const float scale = a.scale;
@@ -520,7 +522,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             }
 
             if constexpr (DBIAS) {
-                float* row = DBt + klocal * a.SqP + q0 + 8 * g;
+                // this lane is the only writer of these eight elements, so the order is fixed
+                // (a read-modify-write: LDS float atomics measured several times slower here)
+                float* row = DBt + klocal * dbld + q0 + 8 * g;
                 float4 lo = *reinterpret_cast<float4*>(row);
                 float4 hi = *reinterpret_cast<float4*>(row + 4);
                 lo.x += dsf[0]; lo.y += dsf[1]; lo.z += dsf[2]; lo.w += dsf[3];
@@ -589,9 +593,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     if constexpr (DBIAS) {
         __syncthreads();
-        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * T::kBK * a.SqP;
-        for (int i = tid * 4; i < T::kBK * a.SqP; i += T::kThreads * 4) {
-            *reinterpret_cast<float4*>(dst + i) = *reinterpret_cast<const float4*>(DBt + i);
+        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * T::kBK;
+        for (int i = tid; i < a.SqA * T::kBK; i += T::kThreads) {
+            dst[i] = DBt[(i % T::kBK) * dbld + i / T::kBK];  // to [SqA][64]
         }
     }
 }
@@ -633,45 +637,45 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
     }
 }
 
-// dbias[h][q][64 kblk + kk] = sum over chunks, in chunk order, of partial[c][h][kblk][kk][q]
+// dbias[h][q][64 kblk + kk] = sum over chunks, in chunk order, of partial[c][h][kblk][q][kk]: a
+// workgroup covers 64 query rows of one key block; a thread four keys (one 16-byte load) of four
+// rows 16 apart
 __global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(BwdArgs a) {
-    __shared__ float tile[64][65];
-    const int qtiles = (a.Sq + 63) / 64;
+    const int qgroups = (a.SqA + 63) / 64;
     const int item = blockIdx.x;
-    const int qt = item % qtiles, rest = item / qtiles;
+    const int qgrp = item % qgroups, rest = item / qgroups;
     const int kblk = rest % a.kblocks, h = rest / a.kblocks;
-    const int tid = threadIdx.x;
-    const int q0 = qt * 64;
-    {
-        const int kk = tid / 4, qc = (tid % 4) * 16;
-        float sum[16];
+    const int k4 = (threadIdx.x & 15) * 4, q0 = qgrp * 64 + (threadIdx.x >> 4);
+    const int64_t stride = (int64_t)a.H * a.kblocks * a.SqA * 64;
+    const float* src = a.partial + ((int64_t)h * a.kblocks + kblk) * a.SqA * 64 + k4;
+    float4 sum[4];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) sum[j] = 0.f;
-        for (int c = 0; c < a.chunks; ++c) {
-            const float* src = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * 64 * a.SqP +
-                               (int64_t)kk * a.SqP + q0 + qc;
+    for (int r = 0; r < 4; ++r) sum[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    // the adds stay in chunk order; unrolling only puts more loads in flight
+#pragma unroll 4
+    for (int c = 0; c < a.chunks; ++c) {
 #pragma unroll
-            for (int j = 0; j < 16; j += 4) {
-                const float4 v4 = *reinterpret_cast<const float4*>(src + j);
-                sum[j] += v4.x;
-                sum[j + 1] += v4.y;
-                sum[j + 2] += v4.z;
-                sum[j + 3] += v4.w;
+        for (int r = 0; r < 4; ++r) {
+            const int q = q0 + 16 * r;
+            if (q < a.SqA) {
+                const float4 v = *reinterpret_cast<const float4*>(src + c * stride + (int64_t)q * 64);
+                sum[r].x += v.x;
+                sum[r].y += v.y;
+                sum[r].z += v.z;
+                sum[r].w += v.w;
             }
         }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) tile[kk][qc + j] = sum[j];
     }
-    __syncthreads();
-    {
-        const int qq = tid / 4, kc = (tid % 4) * 16;
-        const int gq = q0 + qq;
-        if (gq < a.Sq) {
-            float* dst = a.dbias + ((int64_t)h * a.Sq + gq) * a.Sk + kblk * 64;
+    const int key = kblk * 64 + k4;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                if (kblk * 64 + kc + j < a.Sk) dst[kc + j] = tile[kc + j][qq];
-            }
+    for (int r = 0; r < 4; ++r) {
+        const int q = q0 + 16 * r;
+        if (q >= a.Sq) continue;
+        float* dst = a.dbias + ((int64_t)h * a.Sq + q) * a.Sk + key;
+        const float v[4] = {sum[r].x, sum[r].y, sum[r].z, sum[r].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (key + j < a.Sk) dst[j] = v[j];
         }
     }
 }
@@ -702,7 +706,7 @@ static int cu_count(int device) {
 struct BwdPlan {
     int DP = 32;
     int QG = 1;  // query groups of the dK/dV kernel
-    int SqP = 0, kblocks = 0, chunk = 0, chunks = 0;
+    int kblocks = 0, chunk = 0, chunks = 0;
     size_t stage_lds = 0, dbias_lds = 0;
     int SqA = 0, SkA = 0;
     size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0;
@@ -724,10 +728,10 @@ static size_t dkdv_stage_bytes(int DP, int QG) {
 static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
     BwdPlan p;
     p.DP = D <= 32 ? 32 : D <= 64 ? 64 : 96;
-    // rows cover whole 64-query tiles of the reduce kernel; +4 floats staggers LDS banks
-    p.SqP = (int)(((Sq + 63) / 64) * 64 + 4);
+    p.SqA = (int)(((Sq + 31) / 32) * 32);
     p.kblocks = (int)((Sk + 63) / 64);
-    p.dbias_lds = (size_t)64 * p.SqP * sizeof(float);
+    p.SkA = p.kblocks * 64;
+    p.dbias_lds = (size_t)64 * (p.SqA + 4) * sizeof(float);  // the dK/dV kernel's [64][SqA + 4]
     const int limit = shared_limit(device);
     const int qg_max = p.DP == 32 ? 4 : 2;
     p.QG = 0;
@@ -766,11 +770,9 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     }
     p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
-    p.SqA = (int)(((Sq + 31) / 32) * 32);
-    p.SkA = p.kblocks * 64;
     p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // delta, and lse2 after it
     p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(float));
-    p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * 64 * p.SqP * sizeof(float));
+    p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     return p;
 }
 
@@ -815,7 +817,7 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     }
     stage_mark(stream, 3);
     if (want_dbias) {
-        const int64_t g3 = (int64_t)((a.Sq + 63) / 64) * p.kblocks * a.H;
+        const int64_t g3 = (int64_t)((a.SqA + 63) / 64) * p.kblocks * a.H;
         hipLaunchKernelGGL(attn_bwd_dbias_kernel, dim3((unsigned)g3), dim3(256), 0, stream, a);
     } else {
         const int64_t nb = (int64_t)a.H * a.Sq * a.Sk;
@@ -901,7 +903,6 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.biast = reinterpret_cast<float*>(ws + 2 * p.delta_bytes);
     a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
-    a.SqP = p.SqP;
     a.SqA = p.SqA;
     a.SkA = p.SkA;
     a.kblocks = p.kblocks;
