@@ -98,7 +98,7 @@ struct DqTile {
     static constexpr int kWaves = 4, kThreads = kWaves * kWave, kQB = 2;
     static constexpr int kBQ = kWaves * kQB * 16, kBK = 64;
     static constexpr int kKS = DP / 32, kDB = DP / 16;
-    static constexpr int kLd = DP + 8, kTLd = kBK + 8;
+    static constexpr int kLd = DP + 8;
     static constexpr int kChunks = kBK * DP / 8;
     static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
 };
@@ -109,7 +109,6 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
     // two key tiles in flight: one being read by the MFMAs, the next being written
     __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kLd];
     __shared__ __attribute__((aligned(16))) half_t Vs2[2][T::kBK * T::kLd];
-    __shared__ __attribute__((aligned(16))) half_t Kt2[2][DP * T::kTLd];
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -182,9 +181,6 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
                 const int prow = perm_row(row, 16);
                 *reinterpret_cast<half8*>(&Ks2[buf][prow * T::kLd + col]) = kv;
                 *reinterpret_cast<half8*>(&Vs2[buf][prow * T::kLd + col]) = vreg[i];
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    Kt2[buf][(perm_base8(col, DP / 4) + perm_off8(j)) * T::kTLd + row] = kv[j];
             }
         }
     };
@@ -222,7 +218,6 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
     for (int k0 = 0, buf = 0; k0 < a.Sk; k0 += T::kBK, buf ^= 1) {
         const half_t* Ks = Ks2[buf];
         const half_t* Vs = Vs2[buf];
-        const half_t* Kt = Kt2[buf];
         const bool more = k0 + T::kBK < a.Sk;
         BH16 bias16[T::kQB];
 #pragma unroll
@@ -276,7 +271,9 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
-                const half8 kto = bld8(&Kt[(16 * db + r16) * T::kTLd + 16 * g + 8 * kt]);
+                // K^T read transposed from the row-major K tile: slots are keys 16 g + 8 kt + j
+                const half8 kto = lds_operand_tr([&](int r) { return Ks + perm_row(r, 16) * T::kLd; },
+                                                 2 * g + kt, r16, 4 * db, DP / 4);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[kt][qb], acc[db][qb]);
             }
@@ -319,15 +316,16 @@ struct DkdvTile {
     static constexpr int kBK = 64;                    // keys per workgroup, 16 per key group
     static constexpr int kBQ = 32;                    // queries per tile (one contraction step)
     static constexpr int kKS = DP / 32, kDB = DP / 16;
-    static constexpr int kLd = DP + 8, kTLd = kBQ + 8;
+    static constexpr int kLd = DP + 8;
     static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO chunks of one tile
     static constexpr int kCPT = (kChunks + 255) / 256;
-    static constexpr int kStage = 2 * kBQ * kLd + 2 * DP * kTLd;   // halfs per query group
-    static constexpr int kStageBytes = kStage * 2 * QG;
+    static constexpr int kStage = 2 * kBQ * kLd;      // halfs per query group: Q and dO rows
     static constexpr int kCombineBytes = 4 * (QG - 1) * kDB * kWave * 4 * 4;
+    // the staging area, which the end-of-row combine of the query groups reuses
+    static constexpr int kStageBytes =
+        kStage * 2 * QG > kCombineBytes ? kStage * 2 * QG : kCombineBytes;
     // dBias partial [kBK keys][SqA + kDBPad]: the pad staggers the keys' rows across LDS banks
     static constexpr int kDBPad = 4;
-    static_assert(kCombineBytes <= kStageBytes, "the combine reuses the staging area");
 };
 
 template <int DP, int QG, bool DBIAS>
@@ -352,8 +350,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     half_t* Qs = reinterpret_cast<half_t*>(lds_raw) + qg * T::kStage;
     half_t* Os = Qs + T::kBQ * T::kLd;
-    half_t* Qt = Os + T::kBQ * T::kLd;
-    half_t* Ot = Qt + DP * T::kTLd;
     const int dbld = a.SqA + T::kDBPad;
     float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][dbld]
     float* comb = reinterpret_cast<float*>(lds_raw);                   // between rows only
@@ -411,11 +407,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
                 const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
                 half_t* rm = which ? Os : Qs;
-                half_t* tr = which ? Ot : Qt;
                 *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = c.s[i];
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    tr[(perm_base8(col, DP / 4) + perm_off8(j)) * T::kTLd + row] = c.s[i][j];
             }
         }
     };
@@ -511,12 +503,14 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 }
             }
 
-            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4
+            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
+            // its k-slots queries 8 g + j, read transposed from the row-major tiles
+            const auto orow = [&](int r) { return Os + perm_row(r, 8) * T::kLd; };
+            const auto qrow = [&](int r) { return Qs + perm_row(r, 8) * T::kLd; };
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
-                const int drow = 16 * db + r16;  // d (DP/4)(r/4) + 4 db + r%4
-                const half8 ot = bld8(&Ot[drow * T::kTLd + 8 * g]);
-                const half8 qt = bld8(&Qt[drow * T::kTLd + 8 * g]);
+                const half8 ot = lds_operand_tr(orow, g, r16, 4 * db, DP / 4);
+                const half8 qt = lds_operand_tr(qrow, g, r16, 4 * db, DP / 4);
                 accv[db] = mfma16x16x32(ot, pb, accv[db]);
                 acck[db] = mfma16x16x32(qt, dsb, acck[db]);
             }

@@ -45,11 +45,10 @@ struct FwdTile {
     static constexpr int kBK = 64;                    // keys per tile
     static constexpr int kKS = DP / 32;               // contraction steps of S^T
     static constexpr int kDB = DP / 16;               // 16-row blocks of O^T
-    static constexpr int kKsLd = DP + 8;              // K row stride in LDS (halfs)
-    static constexpr int kVtLd = kBK + 8;             // V^T row stride in LDS (halfs)
+    static constexpr int kKsLd = DP + 8;              // K and V row stride in LDS (halfs)
     static constexpr int kChunks = kBK * DP / 8;      // 16-byte chunks in a K (or V) tile
     static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
-    static constexpr int kLds = 2 * (kBK * kKsLd + DP * kVtLd) * 2;
+    static constexpr int kLds = 2 * (2 * kBK * kKsLd) * 2;
 };
 
 struct H16 {
@@ -97,7 +96,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
     using T = FwdTile<DP>;
     // two key tiles in flight: one being read by the MFMAs, the next being written
     __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kKsLd];
-    __shared__ __attribute__((aligned(16))) half_t Vt2[2][DP * T::kVtLd];
+    __shared__ __attribute__((aligned(16))) half_t Vs2[2][T::kBK * T::kKsLd];
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -172,7 +171,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
     };
     const auto stage = [&](int buf) {
         half_t* Ks = Ks2[buf];
-        half_t* Vt = Vt2[buf];
+        half_t* Vs = Vs2[buf];
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
             const int c = tid + i * T::kThreads;
@@ -180,9 +179,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
                 const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
                 *reinterpret_cast<half8*>(&Ks[perm_row(row, 16) * T::kKsLd + col]) =
                     kkeep[i] ? kreg[i] : zero8();
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    Vt[(perm_base8(col, DP / 4) + perm_off8(j)) * T::kVtLd + row] = vreg[i][j];
+                *reinterpret_cast<half8*>(&Vs[row * T::kKsLd + col]) = vreg[i];
             }
         }
     };
@@ -220,7 +217,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
     }
     for (int k0 = 0, buf = 0; k0 < k_end; k0 += T::kBK, buf ^= 1) {
         const half_t* Ks = Ks2[buf];
-        const half_t* Vt = Vt2[buf];
+        const half_t* Vs = Vs2[buf];
         const bool more = k0 + T::kBK < k_end;
         H16 bias16[T::kQB];
 #pragma unroll
@@ -301,12 +298,14 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         }
 
         // O^T += V^T P^T: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4; slot 8 g + j of
-        // contraction step kt is key 16 g + 8 kt + j, which is where P^T already sits
+        // contraction step kt is key 16 g + 8 kt + j, which is where P^T already sits. V^T is
+        // read transposed from the row-major V tile.
+        const auto vrow = [&](int r) { return Vs + r * T::kKsLd; };
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
-                const half8 vop = ld8(&Vt[(16 * db + r16) * T::kVtLd + 16 * g + 8 * kt]);
+                const half8 vop = lds_operand_tr(vrow, 2 * g + kt, r16, 4 * db, DP / 4);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(vop, pb[kt][qb], acc[db][qb]);
             }

@@ -47,6 +47,29 @@ __device__ __forceinline__ int perm_row(int x, int per) {
 __device__ __forceinline__ int perm_base8(int col, int per) { return 4 * (col % per) + 4 * (col / per); }
 __host__ __device__ constexpr int perm_off8(int j) { return 16 * (j >> 2) + (j & 3); }
 
+// gfx950 LDS transpose read (ds_read_b64_tr_b16). Within each group of 16 lanes every lane points
+// at 4 fp16 values (8 bytes, 8-byte aligned); lane i receives in slot j value i % 4 of the 8
+// bytes that lane 4 j + i / 4 points at.
+__device__ __forceinline__ half4 lds_read_tr16(const half_t* p) {
+    typedef short short4v __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) short4v lds_short4;
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_short4*)((__attribute__((address_space(3))) char*)p));
+    return __builtin_bit_cast(half4, r);
+}
+
+// An MFMA operand whose 8 k-slots come from 8 rows of a row-major fp16 tile in LDS: lane i of
+// 16-lane group g gets, for its row index x(i) = `cols` + (i / 4) * cstride + i % 4, the values
+// tile[row(8 g + j)][x(i)] for j = 0..7, where the caller's `at(r)` gives the address of tile row
+// r (after any row permutation). Two transpose reads, 4 rows each.
+template <typename At>
+__device__ __forceinline__ half8 lds_operand_tr(At at, int g, int lane16, int cols, int cstride) {
+    const int j = lane16 >> 2, c = lane16 & 3;
+    const half4 lo = lds_read_tr16(at(8 * g + j) + cols + c * cstride);
+    const half4 hi = lds_read_tr16(at(8 * g + 4 + j) + cols + c * cstride);
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // Pin v as an fp32 register value, so its later rounding to fp16 is a separate step that the
 // compiler cannot fold into the multiply producing v (v_fma_mixlo_f16 rounds once). Every
 // template variant of a kernel then rounds alike, as the reference rounds its fp32 dS.
