@@ -23,6 +23,12 @@ namespace clk {
 constexpr int kFThreads = 256;
 constexpr int kFWaves = kFThreads / kWave;
 constexpr int kTileRows = 64;
+constexpr int kProjThreads = 512;  // the projections' workgroup: 8 waves share the weights
+constexpr int kEpiThreads = 256;   // the tri-mul epilogue's workgroup
+// ln_gdp: at K = 64 three 4-wave workgroups fit a CU (LDS and registers), at K = 128 one, which
+// then runs 8 waves
+template <int K>
+constexpr int gdp_threads() { return K == 64 ? 256 : 512; }
 
 enum TileWork { kCompute = 0, kPadding = 1, kSkip = 2 };
 
@@ -85,19 +91,20 @@ __device__ __forceinline__ void load_weight_frags(half_t* dst, const half_t* W, 
 // R rows of a row-major [M][K] fp16 matrix; 256 / R threads per row, each holding K / (8 TPR)
 // 16-byte chunks (chunk c = part + TPR j). QUAD picks the channel-major A-operand layout
 // (quad_row), otherwise the transposed product's B-operand layout.
-template <int K, int R>
+template <int K, int R, int TH = kFThreads>
 struct RowTile {
-    static constexpr int kTPR = kFThreads / R;
+    static constexpr int kTPR = TH / R;
+    static_assert(K / 8 >= kTPR, "each thread holds at least one 16-byte chunk of its row");
     static constexpr int kChunks = K / 8 / kTPR;
     half8 v[kChunks];
 };
 
-template <int K, int R>
-__device__ __forceinline__ void fetch_rows(RowTile<K, R>& t, const half_t* x, int M, int m0) {
-    constexpr int TPR = RowTile<K, R>::kTPR;
+template <int K, int R, int TH>
+__device__ __forceinline__ void fetch_rows(RowTile<K, R, TH>& t, const half_t* x, int M, int m0) {
+    constexpr int TPR = RowTile<K, R, TH>::kTPR;
     const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
 #pragma unroll
-    for (int j = 0; j < RowTile<K, R>::kChunks; ++j) {
+    for (int j = 0; j < RowTile<K, R, TH>::kChunks; ++j) {
         const int c = part + TPR * j;
         t.v[j] = m0 + row < M ? fld8(x + (int64_t)(m0 + row) * K + 8 * c) : fzero8();
     }
@@ -111,10 +118,10 @@ __device__ __forceinline__ float group_sum(float s) {
     return s;
 }
 
-template <int K, int R, bool QUAD, bool LN>
-__device__ __forceinline__ void ln_rows_to_frags(half_t* Xf, const RowTile<K, R>& t,
+template <int K, int R, bool QUAD, bool LN, int TH>
+__device__ __forceinline__ void ln_rows_to_frags(half_t* Xf, const RowTile<K, R, TH>& t,
                                                  const float* sc, const float* of, float eps) {
-    using RT = RowTile<K, R>;
+    using RT = RowTile<K, R, TH>;
     constexpr int TPR = RT::kTPR, KS = K / 32;
     const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
     float mean = 0.f, rstd = 1.f;
@@ -180,9 +187,12 @@ struct ProjArgs {
     float eps;
 };
 
-template <int K, bool LN>
-__global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
-    constexpr int KS = K / 32;
+// TH threads share the LDS-resident weights. The 64 x ncols output tile is split into items of
+// one column pair (32 outputs) and 4 / split row blocks: with at least as many pairs as waves a
+// wave takes whole pairs, otherwise `split` waves share a pair and divide its four row blocks.
+template <int K, bool LN, int TH>
+__global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
+    constexpr int KS = K / 32, TW = TH / kWave;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     const int col0 = blockIdx.y * a.cols;
     const int ncols = min(a.cols, a.n - col0);
@@ -197,7 +207,7 @@ __global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
     if (npairs > 0) load_weight_frags<K, true>(Wf, a.wT, ncols, 2 * npairs, col0);
     if (do_heads) load_weight_frags<K, false>(Hf, a.wbT, a.heads, 1);
     if constexpr (LN) {
-        for (int i = threadIdx.x; i < K; i += kFThreads) {
+        for (int i = threadIdx.x; i < K; i += TH) {
             sc[i] = a.scale[i];
             of[i] = a.offset[i];
         }
@@ -206,9 +216,12 @@ __global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int tiles = (a.M + kTileRows - 1) / kTileRows;
-    const int head_wave = npairs % kFWaves;
+    const int split = npairs >= TW || npairs == 0 ? 1 : min(4, TW / npairs);
+    const int rbn = 4 / split, rb0 = (wave % split) * rbn;
+    const int pair0 = wave / split, pstride = TW / split;
+    const bool heads_wave = do_heads && wave == TW - 1;
 
-    RowTile<K, kTileRows> xt;
+    RowTile<K, kTileRows, TH> xt;
     if (blockIdx.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, blockIdx.x * kTileRows);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const int m0 = tile * kTileRows;
@@ -217,13 +230,13 @@ __global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
             if (work == kPadding) {
                 // with a residual the output aliases it, which padding keeps
                 if (ncols > 0 && a.residual == nullptr) {
-                    for (int i = threadIdx.x; i < kTileRows * ncols / 8; i += kFThreads) {
+                    for (int i = threadIdx.x; i < kTileRows * ncols / 8; i += TH) {
                         const int r = i / (ncols / 8), c = (i % (ncols / 8)) * 8;
                         if (m0 + r < a.M) fst8(a.out + (int64_t)(m0 + r) * a.n + col0 + c, fzero8());
                     }
                 }
                 if (do_heads) {
-                    for (int i = threadIdx.x; i < kTileRows * a.heads; i += kFThreads) {
+                    for (int i = threadIdx.x; i < kTileRows * a.heads; i += TH) {
                         const int h = i / kTileRows, r = i % kTileRows;
                         if (m0 + r < a.M) a.bias[(int64_t)h * a.M + m0 + r] = (half_t)0.f;
                     }
@@ -241,9 +254,11 @@ __global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
+            for (int ks = 0; ks < KS; ++ks) {
+                if (rb >= rb0 && rb < rb0 + rbn) xop[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
+            }
 
-        for (int cp = wave; cp < npairs; cp += kFWaves) {
+        for (int cp = pair0; cp < npairs; cp += pstride) {
             float4v acc[2][4];
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb)
@@ -255,26 +270,47 @@ __global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
                 for (int hb = 0; hb < 2; ++hb) {
                     const half8 w = fld8(Wf + frag(2 * cp + hb, ks, KS, lane));
 #pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) acc[hb][rb] = mfma16x16x32(w, xop[rb][ks], acc[hb][rb]);
+                    for (int rb = 0; rb < 4; ++rb) {
+                        if (rb >= rb0 && rb < rb0 + rbn) acc[hb][rb] = mfma16x16x32(w, xop[rb][ks], acc[hb][rb]);
+                    }
                 }
             }
             const int col = col0 + 32 * cp + 8 * g;
             float bv[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bv[j] = a.b ? (float)a.b[col + j] : 0.f;
+            for (int j = 0; j < 8; ++j) bv[j] = 0.f;
+            if constexpr (!LN) {
+                const half8 b8 = fld8(a.b + col);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bv[j] = (float)b8[j];
+            }
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
                 const int row = m0 + 16 * rb + r16;
-                if (row >= a.M) continue;
+                if (rb < rb0 || rb >= rb0 + rbn || row >= a.M) continue;
                 half_t* dst = a.out + (int64_t)row * a.n + col;
-                half8 res = a.residual ? fld8(a.residual + (int64_t)row * a.n + col) : fzero8();
                 half8 o;
+                if constexpr (LN) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[j] + (float)res[j]);
+                    for (int j = 0; j < 8; ++j) o[j] = (half_t)acc[j >> 2][rb][j & 3];
+                } else if (a.residual != nullptr) {
+                    const half8 res = fld8(a.residual + (int64_t)row * a.n + col);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[j] + (float)res[j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[j]);
+                }
                 fst8(dst, o);
             }
         }
-        if (do_heads && wave == head_wave) {
+        if (heads_wave) {
+            // the head-bias block reads every row block
+            half8 hx[4][KS];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) hx[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
             float4v acc[4];
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) acc[rb] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -282,7 +318,7 @@ __global__ __launch_bounds__(kFThreads) void proj_kernel(ProjArgs a) {
             for (int ks = 0; ks < KS; ++ks) {
                 const half8 w = fld8(Hf + frag(0, ks, KS, lane));
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma16x16x32(w, xop[rb][ks], acc[rb]);
+                for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma16x16x32(w, hx[rb][ks], acc[rb]);
             }
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
@@ -309,9 +345,9 @@ struct LnGdpArgs {
     float eps;
 };
 
-template <int K>
-__global__ __launch_bounds__(kFThreads) void ln_gdp_kernel(LnGdpArgs a) {
-    constexpr int KS = K / 32;
+template <int K, int TH>
+__global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
+    constexpr int KS = K / 32, TW = TH / kWave;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     const int nb = a.P / 16;
     half_t* Wp = lds;
@@ -321,7 +357,7 @@ __global__ __launch_bounds__(kFThreads) void ln_gdp_kernel(LnGdpArgs a) {
     float* of = sc + K;
     load_weight_frags<K, false>(Wp, a.wpT, a.P, nb);
     load_weight_frags<K, false>(Wg, a.wgT, a.P, nb);
-    for (int i = threadIdx.x; i < K; i += kFThreads) {
+    for (int i = threadIdx.x; i < K; i += TH) {
         sc[i] = a.scale[i];
         of[i] = a.offset[i];
     }
@@ -331,7 +367,7 @@ __global__ __launch_bounds__(kFThreads) void ln_gdp_kernel(LnGdpArgs a) {
     const int ci = a.P / 2;
     const bool vec = (a.M & 7) == 0;
 
-    RowTile<K, kTileRows> xt;
+    RowTile<K, kTileRows, TH> xt;
     if (blockIdx.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, blockIdx.x * kTileRows);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const int m0 = tile * kTileRows;
@@ -339,7 +375,7 @@ __global__ __launch_bounds__(kFThreads) void ln_gdp_kernel(LnGdpArgs a) {
         const int work = tile_work(a.mask, a.M, m0, kTileRows, 0.f);
         if (work != kCompute) {
             if (work == kPadding) {
-                for (int i = threadIdx.x; i < kTileRows * ci; i += kFThreads) {
+                for (int i = threadIdx.x; i < kTileRows * ci; i += TH) {
                     const int c = i / kTileRows, r = i % kTileRows;
                     if (m0 + r < a.M) {
                         a.left[(int64_t)c * a.M + m0 + r] = (half_t)0.f;
@@ -367,7 +403,7 @@ __global__ __launch_bounds__(kFThreads) void ln_gdp_kernel(LnGdpArgs a) {
             const int row = m0 + 16 * g + t;
             mv[t] = row < a.M ? fmaxf((float)a.mask[row], 0.f) : 0.f;
         }
-        for (int cb = wave; cb < nb; cb += kFWaves) {
+        for (int cb = wave; cb < nb; cb += TW) {
             float4v ap[4], ag[4];
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
@@ -423,10 +459,13 @@ struct EpiArgs {
     float eps;
 };
 
-template <int C, int CA, bool ADD>
-__global__ __launch_bounds__(kFThreads) void epilogue_kernel(EpiArgs a) {
-    constexpr int KC = C / 32, KA = CA / 32;
+template <int C, int CA, bool ADD, int TH, bool PREFETCH>
+__global__ __launch_bounds__(TH) void epilogue_kernel(EpiArgs a) {
+    constexpr int KC = C / 32, KA = CA / 32, TW = TH / kWave;
     constexpr int kSub = 32;  // the reference's keep granularity here (volta_gdp.h:41)
+    // column LayerNorm of x_cm: a thread holds one row's values of one of NQ channel groups
+    constexpr int NQ = TH / kTileRows, CQ = C / NQ;
+    static_assert(CQ % 8 == 0, "channel groups are whole 16-byte fragments");
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     const int nb = a.O / 16, npairs = a.O / 32;
     half_t* Wo = lds;
@@ -437,77 +476,88 @@ __global__ __launch_bounds__(kFThreads) void epilogue_kernel(EpiArgs a) {
     float* lof = lsc + C;
     float* isc = lof + C;
     float* iof = isc + CA;
-    float* red = iof + CA;  // [4][64]
+    float* red = iof + CA;  // [NQ][64]
     load_weight_frags<C, true>(Wo, a.woT, a.O, nb);
     load_weight_frags<CA, true>(Wg, a.wgT, a.O, nb);
-    for (int i = threadIdx.x; i < C; i += kFThreads) {
+    for (int i = threadIdx.x; i < C; i += TH) {
         lsc[i] = a.ln_scale[i];
         lof[i] = a.ln_offset[i];
     }
-    for (int i = threadIdx.x; i < CA; i += kFThreads) {
+    for (int i = threadIdx.x; i < CA; i += TH) {
         isc[i] = a.in_scale[i];
         iof[i] = a.in_offset[i];
     }
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int r = threadIdx.x % kTileRows, cq = threadIdx.x / kTileRows;
 
-    RowTile<CA, kTileRows> xt;
+    // this thread's x_cm values and x chunks of a tile, one tile ahead of their use
+    RowTile<CA, kTileRows, TH> xt;
+    float v[CQ];
+    const auto fetch = [&](int m0) {
+        fetch_rows<CA, kTileRows>(xt, a.x, a.M, m0);
+#pragma unroll
+        for (int i = 0; i < CQ; ++i) v[i] = m0 + r < a.M ? a.x_cm[(int64_t)(cq * CQ + i) * a.M + m0 + r] : 0.f;
+    };
+    if (PREFETCH && blockIdx.x < tiles) fetch(blockIdx.x * kTileRows);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const int m0 = tile * kTileRows;
         const int w0 = tile_work(a.keep, a.M, m0, kSub, -1.f);
         const int w1 = tile_work(a.keep, a.M, m0 + kSub, kSub, -1.f);
         if (w0 != kCompute && w1 != kCompute) {
             if (!ADD) {  // with add_input the output aliases x, which padding keeps
-                for (int i = threadIdx.x; i < kTileRows * a.O / 8; i += kFThreads) {
-                    const int r = i / (a.O / 8), c = (i % (a.O / 8)) * 8;
-                    const int w = r < kSub ? w0 : w1;
-                    if (w == kPadding && m0 + r < a.M) fst8(a.out + (int64_t)(m0 + r) * a.O + c, fzero8());
+                for (int i = threadIdx.x; i < kTileRows * a.O / 8; i += TH) {
+                    const int rr = i / (a.O / 8), c = (i % (a.O / 8)) * 8;
+                    const int w = rr < kSub ? w0 : w1;
+                    if (w == kPadding && m0 + rr < a.M) fst8(a.out + (int64_t)(m0 + rr) * a.O + c, fzero8());
                 }
             }
+            if (PREFETCH && tile + gridDim.x < tiles) fetch((tile + gridDim.x) * kTileRows);
             continue;
         }
-        fetch_rows<CA, kTileRows>(xt, a.x, a.M, m0);
-        // column LayerNorm of x_cm[:, m0 .. m0+63]: thread = (row r, channel quarter cq)
-        const int r = threadIdx.x % kTileRows, cq = threadIdx.x / kTileRows;
-        constexpr int CQ = C / 4;
-        float v[CQ];
+        if (!PREFETCH) fetch(m0);
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < CQ; ++i) {
-            v[i] = m0 + r < a.M ? a.x_cm[(int64_t)(cq * CQ + i) * a.M + m0 + r] : 0.f;
-            s += v[i];
-        }
+        for (int i = 0; i < CQ; ++i) s += v[i];
         __syncthreads();  // the previous tile's operand and reduction reads are done
         red[cq * kTileRows + r] = s;
         __syncthreads();
-        const float mean = (red[r] + red[kTileRows + r] + red[2 * kTileRows + r] + red[3 * kTileRows + r]) * (1.f / C);
-        float q = 0.f;
+        float mean = 0.f;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) mean += red[q * kTileRows + r];
+        mean *= 1.f / C;
+        float q2 = 0.f;
+        float d[CQ];
 #pragma unroll
         for (int i = 0; i < CQ; ++i) {
-            v[i] -= mean;
-            q += v[i] * v[i];
+            d[i] = v[i] - mean;
+            q2 += d[i] * d[i];
         }
         __syncthreads();
-        red[cq * kTileRows + r] = q;
+        red[cq * kTileRows + r] = q2;
         __syncthreads();
-        const float var = (red[r] + red[kTileRows + r] + red[2 * kTileRows + r] + red[3 * kTileRows + r]) * (1.f / C);
-        const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
+        float var = 0.f;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) var += red[q * kTileRows + r];
+        const float rstd = __builtin_amdgcn_rsqf(var * (1.f / C) + a.eps);
 #pragma unroll
         for (int i = 0; i < CQ; i += 8) {
             half8 y;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int c = cq * CQ + i + e;
-                y[e] = (half_t)(v[i + e] * rstd * lsc[c] + lof[c]);
+                y[e] = (half_t)(d[i + e] * rstd * lsc[c] + lof[c]);
             }
             const int c = (cq * CQ + i) / 8;
             fst8(Yf + frag(r >> 4, c >> 2, KC, (r & 15) + 16 * (c & 3)), y);
         }
         ln_rows_to_frags<CA, kTileRows, false, true>(Af, xt, isc, iof, a.eps);
         __syncthreads();
+        // with add_input the output aliases x: this tile's x was read (and normalised) above
+        if (PREFETCH && tile + gridDim.x < tiles) fetch((tile + gridDim.x) * kTileRows);
 
-        for (int cp = wave; cp < npairs; cp += kFWaves) {
+        for (int cp = wave; cp < npairs; cp += TW) {
             float4v ao[2][4], ag[2][4];
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb)
@@ -838,14 +888,14 @@ extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buff
     const dim3 grid(persistent_grid(tiles, lds));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (K == 64) {
-        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64>, grid, lds, s, &a, 0)) return st;
+        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64, gdp_threads<64>()>, grid, lds, s, &a, 0)) return st;
         stage_mark(s, 0);
-        hipLaunchKernelGGL(ln_gdp_kernel<64>, grid, dim3(kFThreads), lds, s, a);
+        hipLaunchKernelGGL((ln_gdp_kernel<64, gdp_threads<64>()>), grid, dim3(gdp_threads<64>()), lds, s, a);
         stage_mark(s, 1);
     } else {
-        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<128>, grid, lds, s, &a, 0)) return st;
+        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<128, gdp_threads<128>()>, grid, lds, s, &a, 0)) return st;
         stage_mark(s, 0);
-        hipLaunchKernelGGL(ln_gdp_kernel<128>, grid, dim3(kFThreads), lds, s, a);
+        hipLaunchKernelGGL((ln_gdp_kernel<128, gdp_threads<128>()>), grid, dim3(gdp_threads<128>()), lds, s, a);
         stage_mark(s, 1);
     }
     return launch_status("ln_gdp");
@@ -853,13 +903,15 @@ extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buff
 
 template <int C, int CA, bool ADD>
 static int run_epilogue(const EpiArgs& a, hipStream_t s) {
+    constexpr int TH = kEpiThreads;
     const size_t lds = (size_t)(a.O * C + a.O * CA + kTileRows * C + kTileRows * CA) * 2 +
-                       (size_t)(2 * C + 2 * CA + 4 * kTileRows) * 4;
+                       (size_t)(2 * C + 2 * CA + TH) * 4;
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     const dim3 grid(persistent_grid(tiles, lds));
-    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, ADD>, grid, lds, s, &a, 0)) return st;
+    constexpr bool PF = C == 128;  // measured: the prefetch pays at C = 128 and costs at 64
+    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, ADD, TH, PF>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((epilogue_kernel<C, CA, ADD>), grid, dim3(kFThreads), lds, s, a);
+    hipLaunchKernelGGL((epilogue_kernel<C, CA, ADD, TH, PF>), grid, dim3(TH), lds, s, a);
     stage_mark(s, 1);
     return launch_status("trimul_epilogue");
 }
@@ -919,9 +971,10 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     const size_t lds = (size_t)(std::min(a.cols, std::max(a.n, 0)) * K) * 2 + fixed;
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     const dim3 grid(persistent_grid(tiles, lds), chunks);
-    if (int st = launch_fused(what, proj_kernel<K, LN>, grid, lds, s, &a, 0)) return st;
+    constexpr int TH = kProjThreads;
+    if (int st = launch_fused(what, proj_kernel<K, LN, TH>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((proj_kernel<K, LN>), grid, dim3(kFThreads), lds, s, a);
+    hipLaunchKernelGGL((proj_kernel<K, LN, TH>), grid, dim3(TH), lds, s, a);
     stage_mark(s, 1);
     return launch_status(what);
 }
