@@ -36,8 +36,8 @@ _LIB = "libcolabfold_gfx950.so"
 _TABLE = {
     "attention": ((950, _LIB, "VoltaMma"),),
     "attention_bwd": ((950, _LIB, "VoltaMmaBwd"),),
-    "layer_norm": (),
-    "gated_dual_proj": (),
+    "layer_norm": ((950, _LIB, "VoltaLayerNorm"),),
+    "gated_dual_proj": ((950, _LIB, "VoltaGdp"),),
     "ln_gated_dual_proj": ((950, _LIB, "VoltaLnGdp"),),
     "trimul_epilogue": ((950, _LIB, "VoltaTrimulEpilogue"),),
     "ln_projection": ((950, _LIB, "VoltaLnProj"),),

@@ -10,6 +10,8 @@ stream, with the FFI binding's buffer order, attributes, result shapes and error
   ln_projection       VoltaLnProj         (volta_fused_ffi.h:373-388)
   output_projection   VoltaOutProj        (volta_fused_ffi.h:390-401)
   transition          VoltaTransition     (volta_fused_ffi.h:403-418)
+  layer_norm          VoltaLayerNorm      (cuda/volta_ops.cu:86-94)
+  gated_dual_proj     VoltaGdp            (volta_ops.cu:258-269)
 
 Results are allocated here with torch (as XLA preallocates them) unless passed in, which is how a
 caller aliases an output to its residual / input. A rejected call raises InvalidArgument (the
@@ -63,6 +65,8 @@ _SIGNATURES = {
     "clk_output_projection": [ctypes.c_void_p] + [_P] * 6 + [ctypes.c_int32, ctypes.c_int32],
     "clk_transition": [ctypes.c_void_p] + [_P] * 9 +
                       [ctypes.c_float, ctypes.c_int32, ctypes.c_int32],
+    "clk_layer_norm": [ctypes.c_void_p] + [_P] * 4 + [ctypes.c_float],
+    "clk_gated_dual_proj": [ctypes.c_void_p, ctypes.c_int32] + [_P] * 7 + [ctypes.c_int64],
 }
 
 
@@ -238,4 +242,22 @@ def transition(x, scale, offset, w1T, b1, w2T, b2, keep=None, eps=1e-5, add_inpu
     bufs = [buffer(t) for t in (x, scale, offset, w1T, b1, w2T, b2, keep, out)]
     _check(lib().clk_transition(_stream(x), *map(_ref, bufs), float(eps), int(bool(add_input)),
                                 int(has_keep)))
+    return out
+
+
+def layer_norm(x, scale, offset, eps=1e-5, out=None):
+    """VoltaLayerNorm: out [M,C] F16, one-pass fp32 statistics."""
+    out = torch.empty_like(x) if out is None else out
+    bufs = [buffer(t) for t in (x, scale, offset, out)]
+    _check(lib().clk_layer_norm(_stream(x), *map(_ref, bufs), float(eps)))
+    return out
+
+
+def gated_dual_proj(x, wp, bp, wg, bg, mask, activation=0, out=None):
+    """VoltaGdp: out [M,N] = mask * (x@wp + bp) * act(x@wg + bg); wp, wg [K,N];
+    activation 0 sigmoid, 1 swish."""
+    m, n = x.shape[0], wp.shape[1]
+    out = torch.empty((m, n), dtype=torch.float16, device=x.device) if out is None else out
+    bufs = [buffer(t) for t in (x, wp, bp, wg, bg, mask, out)]
+    _check(lib().clk_gated_dual_proj(_stream(x), x.device.index, *map(_ref, bufs), int(activation)))
     return out

@@ -1,9 +1,9 @@
-// XLA FFI handler symbols of the reference's nine targets, over the library's C ABI.
+// XLA FFI handler symbols of the reference's targets on this path, over the library's C ABI.
 //
 // Each exported `XLA_FFI_Error* Name(XLA_FFI_CallFrame*)` decodes the call frame the way the
 // reference's XLA_FFI_DEFINE_HANDLER_SYMBOL bindings declare it (context, arguments, results and
-// attributes in the orders of cuda/volta_mma_attn.cu:594-640, cuda/volta_mma_attn_bwd.cu:455-473
-// and cuda/volta_fused_ffi.h:337-418) and calls the matching clk_* entry point on the stream XLA
+// attributes in the orders of cuda/volta_mma_attn.cu:594-640, cuda/volta_mma_attn_bwd.cu:455-473,
+// cuda/volta_fused_ffi.h:337-418 and cuda/volta_ops.cu:86-94, 258-269) and calls the matching clk_* entry point on the stream XLA
 // provides. It answers XLA's metadata query with API version 0.1 and the reference's traits:
 // every target is command-buffer compatible except VoltaMmaBwd. The backward's workspace comes
 // from XLA's device allocator for the duration of the call, as the reference's ScratchAllocator
@@ -328,6 +328,29 @@ XLA_FFI_Error* VoltaTransition(XLA_FFI_CallFrame* cf) {
     if (!f.stream(&s)) return f.pending();
     return f.status(clk_transition(s, &b[0], &b[1], &b[2], &b[3], &b[4], &b[5], &b[6], &b[7], &b[8],
                                    eps, add_input, has_keep));
+}
+
+XLA_FFI_Error* VoltaLayerNorm(XLA_FFI_CallFrame* cf) {
+    if (preamble(cf, kCmdBuffer)) return nullptr;
+    Frame f(cf);
+    clk_buffer b[4];
+    float eps;
+    if (!f.buffers(3, 1, b) || !f.f32("eps", &eps)) return f.decode_error();
+    clk_stream s;
+    if (!f.stream(&s)) return f.pending();
+    return f.status(clk_layer_norm(s, &b[0], &b[1], &b[2], &b[3], eps));
+}
+
+XLA_FFI_Error* VoltaGdp(XLA_FFI_CallFrame* cf) {
+    if (preamble(cf, kCmdBuffer)) return nullptr;
+    Frame f(cf);
+    clk_buffer b[7];
+    int64_t activation;
+    if (!f.buffers(6, 1, b) || !f.i64("activation", &activation)) return f.decode_error();
+    clk_stream s;
+    if (!f.stream(&s)) return f.pending();
+    return f.status(clk_gated_dual_proj(s, Frame::device_of(s), &b[0], &b[1], &b[2], &b[3], &b[4],
+                                        &b[5], &b[6], activation));
 }
 
 }  // extern "C"

@@ -141,6 +141,22 @@ int clk_transition(clk_stream stream, const clk_buffer* x, const clk_buffer* sca
                    const clk_buffer* w2T, const clk_buffer* b2, const clk_buffer* keep,
                    const clk_buffer* out, float eps, int32_t add_input, int32_t has_keep);
 
+/* ---- unfused pair-stack ops (reference cuda/volta_ops.cu) ------------------------------ */
+
+/* VoltaLayerNorm (volta_ops.cu:27-84, handler 86-94): out [M,C] = LN(x) over the last axis with
+ * one-pass fp32 statistics (var = max(E[x^2] - mean^2, 0)). x [M,C] F16; scale, offset [C] F32;
+ * out [M,C] F16. */
+int clk_layer_norm(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
+                   const clk_buffer* offset, const clk_buffer* out, float eps);
+
+/* VoltaGdp (volta_ops.cu:97-256, handler 258-269): out [M,N] = mask * (x@wp + bp) *
+ * act(x@wg + bg), act = sigmoid (activation 0) or swish (1). x [M,K]; wp, wg [K,N] row-major;
+ * bp, bg [N]; mask [M]; all F16. N a multiple of 8. */
+int clk_gated_dual_proj(clk_stream stream, int32_t device, const clk_buffer* x,
+                        const clk_buffer* wp, const clk_buffer* bp, const clk_buffer* wg,
+                        const clk_buffer* bg, const clk_buffer* mask, const clk_buffer* out,
+                        int64_t activation);
+
 #ifdef __cplusplus
 }
 #endif

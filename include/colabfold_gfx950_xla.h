@@ -1,6 +1,6 @@
 /* colabfold_gfx950_xla.h: the XLA FFI handler symbols of the gfx950 library.
  *
- * The same nine names the reference's libraries export through XLA_FFI_DEFINE_HANDLER_SYMBOL,
+ * The same names the reference's libraries export through XLA_FFI_DEFINE_HANDLER_SYMBOL,
  * each with the reference's binding (context, arguments, results and attributes, in order) and
  * traits. A JAX caller registers them with
  *     jax.ffi.register_ffi_target(name, jax.ffi.pycapsule(fn), platform="ROCM")
@@ -52,6 +52,14 @@ struct XLA_FFI_Error* VoltaOutProj(struct XLA_FFI_CallFrame* call_frame);
 /* volta_fused_ffi.h:403-418. args F16, F32, F32, F16, F16, F16, F16, F16; ret F16;
  * attrs eps, add_input, has_keep. */
 struct XLA_FFI_Error* VoltaTransition(struct XLA_FFI_CallFrame* call_frame);
+
+/* cuda/volta_ops.cu:86-94. args x F16, scale F32, offset F32; ret F16; attr eps.
+ * Command-buffer compatible. */
+struct XLA_FFI_Error* VoltaLayerNorm(struct XLA_FFI_CallFrame* call_frame);
+
+/* volta_ops.cu:258-269. ctx stream, device; args x, wp, bp, wg, bg, mask F16; ret F16;
+ * attr activation i64. Command-buffer compatible. */
+struct XLA_FFI_Error* VoltaGdp(struct XLA_FFI_CallFrame* call_frame);
 
 #ifdef __cplusplus
 }

@@ -8,6 +8,9 @@ Closed forms restated from the reference kernels (their epilogues and FFI commen
   ln_projection      cuda/volta_fused_ffi.h:135-136, cuda/volta_ops.cu:503-541, volta_gdp.h:288-332
   output_projection  cuda/volta_fused_ffi.h:178, cuda/volta_ops.cu:513-541 (LN = false)
   transition         cuda/volta_fused_ffi.h:216-217, cuda/volta_ops.cu:585-634
+  layer_norm_onepass cuda/volta_ops.cu:27-57 (VoltaLayerNorm: one-pass statistics, var clamped at 0)
+  gated_dual_proj    cuda/volta_ops.cu:97-187, volta_gdp.h:10-35 (VoltaGdp: wp, wg [K, N],
+                     out = mask (x@wp + bp) act(x@wg + bg), act sigmoid or swish)
   keep / tile_work   cuda/volta_gdp.h:114-160 and the padding branches at volta_ops.cu:349-356,
                      422-428, 491-502, 578-584
 
@@ -16,7 +19,7 @@ float64): the LayerNorm output is fp16 before its GEMM (volta_gdp.h:237, 283-284
 hidden activation is fp16 (volta_ops.cu:602-604), and the head-bias dot reads the fp16 LN output
 (volta_gdp.h:307-320). Every GEMM accumulates in fp32 in the kernels and in float64 here.
 
-Pinned by (tests/test_oracle_fused.py): torch float64 layer_norm; numpy matmul against an
+Pinned by (tests/test_oracle_fused.py): torch float64 layer_norm (both LN forms); numpy matmul against an
 explicit per-element sum on tiny shapes; the transition's blocked w2T layout against a direct
 gather; the keep rule against a brute-force per-row statement of the reference's tile decision;
 and the committed golden fixtures.
@@ -171,3 +174,21 @@ def transition(x, scale, offset, w1T, b1, w2T, b2, keep, eps, add_input, round_m
     work = tile_work(keep, out.shape[0], rows, -1.0)
     return _apply_keep(out, work, rows, None if add_input else 0.0)
 
+
+def layer_norm_onepass(x, scale, offset, eps):
+    """VoltaLayerNorm over the last axis: mean = E[x], var = max(E[x^2] - mean^2, 0),
+    rstd = 1/sqrt(var + eps) (cuda/volta_ops.cu:40-56), evaluated in float64."""
+    x = np.asarray(x, np.float64)
+    mean = x.mean(-1, keepdims=True)
+    var = np.maximum((x * x).mean(-1, keepdims=True) - mean * mean, 0.0)
+    return (x - mean) / np.sqrt(var + eps) * np.asarray(scale, np.float64) + np.asarray(offset, np.float64)
+
+
+def gated_dual_proj(x, wp, bp, wg, bg, mask, activation):
+    """VoltaGdp: out [M, N] = mask[m] (x@wp + bp) act(x@wg + bg) with wp, wg [K, N]; act is
+    sigmoid (0) or swish, g sigmoid(g) (1) (cuda/volta_ops.cu:168-186, volta_gdp.h:13-19)."""
+    x = np.asarray(x, np.float64)
+    p = x @ np.asarray(wp, np.float64) + np.asarray(bp, np.float64)
+    g = x @ np.asarray(wg, np.float64) + np.asarray(bg, np.float64)
+    act = sigmoid(g) if activation == 0 else g * sigmoid(g)
+    return np.asarray(mask, np.float64)[:, None] * p * act

@@ -6,9 +6,10 @@ import pytest
 
 import colabfold_legacy_kernels as clk
 
-BUILT = ("attention", "attention_bwd", "ln_gated_dual_proj", "trimul_epilogue", "ln_projection",
-         "output_projection", "transition")
-SYMBOLS = {"attention": "VoltaMma", "attention_bwd": "VoltaMmaBwd", "ln_gated_dual_proj": "VoltaLnGdp",
+BUILT = ("attention", "attention_bwd", "layer_norm", "gated_dual_proj", "ln_gated_dual_proj",
+         "trimul_epilogue", "ln_projection", "output_projection", "transition")
+SYMBOLS = {"attention": "VoltaMma", "attention_bwd": "VoltaMmaBwd", "layer_norm": "VoltaLayerNorm",
+           "gated_dual_proj": "VoltaGdp", "ln_gated_dual_proj": "VoltaLnGdp",
            "trimul_epilogue": "VoltaTrimulEpilogue", "ln_projection": "VoltaLnProj",
            "output_projection": "VoltaOutProj", "transition": "VoltaTransition"}
 

@@ -152,3 +152,33 @@ def test_golden_fixtures():
     }
     for name, arr in got.items():
         np.testing.assert_allclose(arr, f[name], rtol=1e-12, atol=1e-12, equal_nan=True, err_msg=name)
+
+
+def test_layer_norm_onepass_matches_torch_and_clamps():
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((23, 100)) * 2 + 0.5
+    sc, of = rng.standard_normal(100), rng.standard_normal(100)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x), (100,), torch.from_numpy(sc),
+                                          torch.from_numpy(of), EPS).numpy()
+    np.testing.assert_allclose(orf.layer_norm_onepass(x, sc, of, EPS), want, rtol=1e-9, atol=1e-9)
+    # a constant row: E[x^2] - mean^2 is zero (or a rounding below it, clamped), so out = offset
+    const = np.full((2, 64), 3.25)
+    np.testing.assert_allclose(orf.layer_norm_onepass(const, np.ones(64), of[:64], EPS),
+                               np.broadcast_to(of[:64], (2, 64)), atol=1e-12)
+
+
+def test_gated_dual_proj_elements():
+    rng = np.random.default_rng(11)
+    M, K, N = 9, 5, 8
+    x, wp, wg = rng.standard_normal((M, K)), rng.standard_normal((K, N)), rng.standard_normal((K, N))
+    bp, bg, mask = rng.standard_normal(N), rng.standard_normal(N), rng.standard_normal(M)
+    for act in (0, 1):
+        out = orf.gated_dual_proj(x, wp, bp, wg, bg, mask, act)
+        for m, n in ((0, 0), (8, 7), (4, 3)):
+            p = sum(x[m, k] * wp[k, n] for k in range(K)) + bp[n]
+            g = sum(x[m, k] * wg[k, n] for k in range(K)) + bg[n]
+            s = 1.0 / (1.0 + np.exp(-g))
+            assert abs(out[m, n] - mask[m] * p * (s if act == 0 else g * s)) < 1e-12
+    # a zero mask row zeroes its outputs
+    mask[2] = 0.0
+    assert np.abs(orf.gated_dual_proj(x, wp, bp, wg, bg, mask, 1)[2]).max() == 0.0

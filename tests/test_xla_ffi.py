@@ -12,7 +12,8 @@ import ffi_frames as ff
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HANDLERS = ("VoltaMma", "VoltaMmaPacked", "VoltaMmaPackedTrim", "VoltaMmaBwd", "VoltaLnGdp",
-            "VoltaTrimulEpilogue", "VoltaLnProj", "VoltaOutProj", "VoltaTransition")
+            "VoltaTrimulEpilogue", "VoltaLnProj", "VoltaOutProj", "VoltaTransition",
+            "VoltaLayerNorm", "VoltaGdp")
 FAKE = 0x100000  # never dereferenced
 
 
@@ -135,3 +136,24 @@ def test_fused_validation_through_handlers(lib):
     rets = [(ff.F16, FAKE, (0, 64))]
     attrs = {"has_residual": (ff.PRED, 0), "has_keep": (ff.PRED, 0)}
     assert mock.call(lib.VoltaOutProj, args, rets, attrs) is None
+
+
+def test_plain_ops_validation_through_handlers(lib):
+    mock = ff.MockXla()
+    x = (ff.F16, FAKE, (10, 64))
+    w = (ff.F16, FAKE, (64, 36))
+    b = (ff.F16, FAKE, (36,))
+    args = [x, w, b, w, b, (ff.F16, FAKE, (10,))]
+    assert mock.call(lib.VoltaGdp, args, [(ff.F16, FAKE, (10, 36))], {"activation": (ff.S64, 0)}) is not None
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT, "gdp: N must be a multiple of 8")
+    w = (ff.F16, FAKE, (64, 32))
+    b = (ff.F16, FAKE, (32,))
+    args = [x, w, b, w, b, (ff.F16, FAKE, (10,))]
+    assert mock.call(lib.VoltaGdp, args, [(ff.F16, FAKE, (10, 32))], {"activation": (ff.S64, 2)}) is not None
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT, "gdp: activation is 0 (sigmoid) or 1 (swish), got 2")
+    args = [(ff.F16, FAKE, (10, 64, 2)), (ff.F32, FAKE, (64,)), (ff.F32, FAKE, (64,))]
+    assert mock.call(lib.VoltaLayerNorm, args, [(ff.F16, FAKE, (10, 64, 2))], {"eps": (ff.F32, 1e-5)}) is not None
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT, "x must be [M,C]")
+    # an empty batch succeeds without a launch
+    args = [(ff.F16, FAKE, (0, 64)), (ff.F32, FAKE, (64,)), (ff.F32, FAKE, (64,))]
+    assert mock.call(lib.VoltaLayerNorm, args, [(ff.F16, FAKE, (0, 64))], {"eps": (ff.F32, 1e-5)}) is None

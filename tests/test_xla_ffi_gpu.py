@@ -149,3 +149,25 @@ def test_fused_handlers(hip):
                   attrs) is None
     assert same(out, ref)
     assert not m.errors
+
+
+def test_plain_handlers(hip):
+    torch.manual_seed(3)
+    lib = hip.lib()
+    M, K, N = 150, 64, 96
+    x = g(M, K)
+    sc, of = g(K, s=.1, mean=1., dtype=torch.float32), g(K, s=.1, dtype=torch.float32)
+    m = mock()
+    ref = hip.layer_norm(x, sc, of, 1e-5)
+    out = torch.empty_like(ref)
+    assert m.call(lib.VoltaLayerNorm, [b(x), b(sc), b(of)], [b(out)], {"eps": (ff.F32, 1e-5)}) is None
+    assert same(out, ref)
+    wp, wg, bp, bg = g(K, N, s=.1), g(K, N, s=.1), g(N, s=.1), g(N, s=.1)
+    mask = torch.ones(M, dtype=torch.float16, device="cuda")
+    for act in (0, 1):
+        ref = hip.gated_dual_proj(x, wp, bp, wg, bg, mask, activation=act)
+        out = torch.empty_like(ref)
+        assert m.call(lib.VoltaGdp, [b(t) for t in (x, wp, bp, wg, bg, mask)], [b(out)],
+                      {"activation": (ff.S64, act)}) is None
+        assert same(out, ref)
+    assert not m.errors
