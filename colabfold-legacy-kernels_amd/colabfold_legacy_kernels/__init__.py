@@ -32,7 +32,7 @@ _CAPABILITIES = (950,)
 _LIB = "libcolabfold_gfx950.so"
 
 # Each kernel lists its libraries from the highest capability first, as the reference's table
-# does. A kernel with no gfx950 row is not built yet: available(950) is then False.
+# does.
 _TABLE = {
     "attention": ((950, _LIB, "VoltaMma"),),
     "attention_bwd": ((950, _LIB, "VoltaMmaBwd"),),
@@ -43,8 +43,8 @@ _TABLE = {
     "ln_projection": ((950, _LIB, "VoltaLnProj"),),
     "output_projection": ((950, _LIB, "VoltaOutProj"),),
     "transition": ((950, _LIB, "VoltaTransition"),),
-    "opm_update": (),
-    "opm_outer": (),
+    "opm_update": ((950, _LIB, "VoltaOpmUpdate"),),
+    "opm_outer": ((950, _LIB, "VoltaOpmOuter"),),
 }
 
 KERNELS = tuple(_TABLE)

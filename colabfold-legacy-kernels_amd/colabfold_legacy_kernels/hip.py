@@ -67,6 +67,8 @@ _SIGNATURES = {
                       [ctypes.c_float, ctypes.c_int32, ctypes.c_int32],
     "clk_layer_norm": [ctypes.c_void_p] + [_P] * 4 + [ctypes.c_float],
     "clk_gated_dual_proj": [ctypes.c_void_p, ctypes.c_int32] + [_P] * 7 + [ctypes.c_int64],
+    "clk_opm_update": [ctypes.c_void_p] + [_P] * 6 + [ctypes.c_float, ctypes.c_int32],
+    "clk_opm_outer": [ctypes.c_void_p] + [_P] * 4,
 }
 
 
@@ -260,4 +262,25 @@ def gated_dual_proj(x, wp, bp, wg, bg, mask, activation=0, out=None):
     out = torch.empty((m, n), dtype=torch.float16, device=x.device) if out is None else out
     bufs = [buffer(t) for t in (x, wp, bp, wg, bg, mask, out)]
     _check(lib().clk_gated_dual_proj(_stream(x), x.device.index, *map(_ref, bufs), int(activation)))
+    return out
+
+
+def opm_update(lhs, t, bias, norm, residual=None, eps=1e-3, out=None):
+    """VoltaOpmUpdate: out [B,D,F] = (lhs@t[:, d] + bias) / (eps + norm[b, d]) (+ residual);
+    lhs [B,K], t [K,D,F] fp16, bias [F], norm [B,D] fp32. residual may be `out` itself."""
+    b, (d, f) = lhs.shape[0], t.shape[1:]
+    out = torch.empty((b, d, f), dtype=torch.float16, device=lhs.device) if out is None else out
+    res = residual if residual is not None else torch.zeros(1, dtype=torch.float16, device=lhs.device)
+    bufs = [buffer(x) for x in (lhs, t, bias, norm, res, out)]
+    _check(lib().clk_opm_update(_stream(lhs), *map(_ref, bufs), float(eps), int(residual is not None)))
+    return out
+
+
+def opm_outer(left, right, wT, out=None):
+    """VoltaOpmOuter: out [B,D,F] = sum_c,e f16(sum_a left[a,b,c] right[a,d,e]) wT[f, c*32 + e];
+    left [16,B,C], right [16,D,32], wT [F, 32 C], all fp16."""
+    b, d, f = left.shape[1], right.shape[1], wT.shape[0]
+    out = torch.empty((b, d, f), dtype=torch.float16, device=left.device) if out is None else out
+    bufs = [buffer(x) for x in (left, right, wT, out)]
+    _check(lib().clk_opm_outer(_stream(left), *map(_ref, bufs)))
     return out

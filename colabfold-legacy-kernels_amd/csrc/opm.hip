@@ -1,0 +1,272 @@
+// The outer product mean kernels for gfx950 (CDNA4): opm_update and opm_outer (reference
+// cuda/volta_ops.cu:643-792, handlers cuda/volta_fused_ffi.h:261-335, 420-440).
+//
+//   opm_update  out[b, d, f] = fp16((sum_k lhs[b, k] t[k, d, f] + bias[f]) / (eps + norm[b, d])
+//               [+ residual[b, d, f]]), fp32 accumulation. A GEMM over N = D F columns: a
+//               workgroup computes a 64 (b) x 64 (n) tile as out^T = t^T lhs^T on MFMA, K steps of
+//               32 staging lhs and t row-major in LDS; the t^T operand is read with the gfx950
+//               transpose load.
+//   opm_outer   out[b, d, f] = fp16(sum_c sum_e fp16(sum_a left[a, b, c] right[a, d, e])
+//               w[c E + e, f]) over the 16 rows a, E = 32, wT [F, C E]. A workgroup owns 16 rows b
+//               and 4 columns d, one wave per d. For each channel c the wave forms
+//               G^T[e, b] = sum_a right[a, d, e] left[a, b, c] with a 16x16x16 MFMA whose A rows
+//               are e in pair order, so that the accumulator, rounded to fp16, is already the B
+//               operand (k-slots e) of out^T[f, b] += W_c^T G_c^T, a 16x16x32 MFMA against the
+//               channel's weight rows staged in LDS. The [B, C E, D] product is never formed.
+#include "clk_common.h"
+
+namespace clk {
+
+__device__ __forceinline__ float4v mfma16x16x16(half4 a, half4 b, float4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// ---- opm_update ---------------------------------------------------------------------------
+
+struct OpmUpdateArgs {
+    const half_t *lhs, *t, *residual;  // lhs [B, K], t [K, D F], residual [B, D F] or null
+    const float *bias, *norm;          // bias [F], norm [B, D]
+    half_t* out;                       // [B, D F]
+    int B, K, D, F;
+    float eps;
+};
+
+constexpr int kUpBM = 64, kUpBN = 64, kUpBK = 32;
+constexpr int kUpXLd = kUpBK + 8, kUpTLd = kUpBN + 8;
+
+// Four waves; wave w owns columns n0 + 16 w .. +15 for all 64 rows (four 16-row blocks).
+__global__ __launch_bounds__(256) void opm_update_kernel(OpmUpdateArgs a) {
+    __shared__ __attribute__((aligned(16))) half_t Xs[kUpBM * kUpXLd];
+    __shared__ __attribute__((aligned(16))) half_t Ts[kUpBK * kUpTLd];
+    const int N = a.D * a.F;
+    const int n0 = blockIdx.x * kUpBN, m0 = blockIdx.y * kUpBM;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+
+    float4v acc[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) acc[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < a.K; k0 += kUpBK) {  // K is a multiple of 32
+        __syncthreads();
+        {
+            const int xr = tid >> 2, xc = (tid & 3) * 8;
+            const int gm = m0 + xr;
+            const half8 xv = gm < a.B ? *reinterpret_cast<const half8*>(a.lhs + (int64_t)gm * a.K + k0 + xc)
+                                      : half8{};
+            *reinterpret_cast<half8*>(&Xs[xr * kUpXLd + xc]) = xv;
+            const int tr = tid >> 3, tc = (tid & 7) * 8;
+            // N = D F is a multiple of 16: a chunk of 8 columns is wholly in or out
+            const half8 tv = n0 + tc < N ? *reinterpret_cast<const half8*>(a.t + (int64_t)(k0 + tr) * N + n0 + tc)
+                                         : half8{};
+            *reinterpret_cast<half8*>(&Ts[tr * kUpTLd + tc]) = tv;
+        }
+        __syncthreads();
+        const half8 top = lds_operand_tr([&](int r) { return Ts + r * kUpTLd; }, g, r16, 16 * wave, 4);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const half8 xb = *reinterpret_cast<const half8*>(&Xs[(16 * rb + r16) * kUpXLd + 8 * g]);
+            acc[rb] = mfma16x16x32(top, xb, acc[rb]);
+        }
+    }
+    // lane holds out[b][n .. n+3], b = m0 + 16 rb + r16, n = n0 + 16 wave + 4 g (one d: F >= 16)
+    const int n = n0 + 16 * wave + 4 * g;
+    if (n >= N) return;
+    const int d = n / a.F, f = n - d * a.F;
+    float bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bv[i] = a.bias[f + i];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        const int b = m0 + 16 * rb + r16;
+        if (b >= a.B) continue;
+        const float den = a.eps + a.norm[(int64_t)b * a.D + d];
+        const int64_t o = (int64_t)b * N + n;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (acc[rb][i] + bv[i]) / den;
+        if (a.residual != nullptr) {  // may alias out: read before the write below
+            const half4 r = *reinterpret_cast<const half4*>(a.residual + o);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += (float)r[i];
+        }
+        half4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = (half_t)v[i];
+        *reinterpret_cast<half4*>(a.out + o) = h;
+    }
+}
+
+// ---- opm_outer ----------------------------------------------------------------------------
+
+constexpr int kOpmRows = 16, kOpmE = 32, kOpmB = 16, kOpmD = 4, kOpmChunk = 16;
+constexpr int kLtLd = kOpmRows + 4;  // Lt[c][b][a] row stride (halfs), 8-byte aligned rows
+
+struct OpmOuterArgs {
+    const half_t *left, *right, *wT;  // left [16, B, C], right [16, D, 32], wT [F, 32 C]
+    half_t* out;                      // [B, D, F]
+    int B, C, D;
+};
+
+// e of A row r in e block eb of the first product: lane group g of its accumulator then holds
+// e = 8 g + 4 eb + i, i.e. the k-slots 8 g .. 8 g + 7 of the second product's B operand
+__device__ __forceinline__ int opm_e(int eb, int r) { return 8 * (r >> 2) + 4 * eb + (r & 3); }
+
+template <int F>
+__global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
+    constexpr int FB = F / 16;
+    constexpr int kWLd = kOpmE + 8;  // Ws row stride (halfs)
+    __shared__ __attribute__((aligned(16))) half_t Lt[kOpmChunk * kOpmB * kLtLd];
+    __shared__ __attribute__((aligned(16))) half_t Ws[2][F * kWLd];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int b0 = blockIdx.x * kOpmB, d = blockIdx.y * kOpmD + wave;
+
+    // right[:, d] as the A operand of the first product: row r of e block eb is e = opm_e(eb, r),
+    // k-slots a = 4 g .. 4 g + 3
+    half4 ra[2];
+#pragma unroll
+    for (int eb = 0; eb < 2; ++eb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            ra[eb][j] = a.right[((int64_t)(4 * g + j) * a.D + d) * kOpmE + opm_e(eb, r16)];
+
+    // the weight rows of channel c: Ws[f][e] = wT[f][32 c + e]
+    const auto stage_w = [&](int buf, int c) {
+        for (int i = tid; i < F * (kOpmE / 8); i += 256) {
+            const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
+            *reinterpret_cast<half8*>(&Ws[buf][f * kWLd + e8]) =
+                *reinterpret_cast<const half8*>(a.wT + (int64_t)f * a.C * kOpmE + c * kOpmE + e8);
+        }
+    };
+    // left[a][b0 + b][c0 .. c0 + 15] to Lt[c][b][a], rows b past B zero
+    const auto stage_left = [&](int c0) {
+        for (int i = tid; i < kOpmRows * kOpmB * (kOpmChunk / 8); i += 256) {
+            const int v = i % (kOpmChunk / 8), b = i / (kOpmChunk / 8) % kOpmB, r = i / (kOpmChunk / 8) / kOpmB;
+            const half8 x = b0 + b < a.B
+                                ? *reinterpret_cast<const half8*>(a.left + ((int64_t)r * a.B + b0 + b) * a.C + c0 + 8 * v)
+                                : half8{};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Lt[((8 * v + j) * kOpmB + b) * kLtLd + r] = x[j];
+        }
+    };
+
+    float4v acc[FB];
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb) acc[fb] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    stage_w(0, 0);
+    for (int c = 0; c < a.C; ++c) {
+        const int cl = c % kOpmChunk, buf = c & 1;
+        if (cl == 0) {
+            __syncthreads();  // the previous chunk's Lt reads are done
+            stage_left(c);
+        }
+        __syncthreads();  // Lt of this chunk and Ws[buf] of this channel are staged
+        if (c + 1 < a.C) stage_w(buf ^ 1, c + 1);  // read a channel ago, before the barrier above
+
+        // G^T[e][b] for this channel: B operand L^T (lane column b, k-slots a = 4 g .. 4 g + 3)
+        const half4 lb = *reinterpret_cast<const half4*>(&Lt[(cl * kOpmB + r16) * kLtLd + 4 * g]);
+        half8 gop;
+#pragma unroll
+        for (int eb = 0; eb < 2; ++eb) {
+            const float4v gt = mfma16x16x16(ra[eb], lb, float4v{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; ++i) gop[4 * eb + i] = (half_t)gt[i];  // the f16 outer product
+        }
+        // out^T[f][b] += W^T G^T: A row r of f block fb is f = 16 fb + r, k-slots e = 8 g + j
+#pragma unroll
+        for (int fb = 0; fb < FB; ++fb) {
+            const half8 w = *reinterpret_cast<const half8*>(&Ws[buf][(16 * fb + r16) * kWLd + 8 * g]);
+            acc[fb] = mfma16x16x32(w, gop, acc[fb]);
+        }
+    }
+    // lane holds out[b][d][f .. f+3], b = b0 + r16, f = 16 fb + 4 g
+    const int b = b0 + r16;
+    if (b >= a.B) return;
+#pragma unroll
+    for (int fb = 0; fb < FB; ++fb) {
+        half4 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = (half_t)acc[fb][i];
+        *reinterpret_cast<half4*>(a.out + ((int64_t)b * a.D + d) * F + 16 * fb + 4 * g) = h;
+    }
+}
+
+static bool opm_width(int64_t f) { return f == 16 || f == 32 || f == 64 || f == 128; }
+
+}  // namespace clk
+
+using namespace clk;
+
+extern "C" int clk_opm_update(clk_stream stream, const clk_buffer* lhs, const clk_buffer* t,
+                              const clk_buffer* bias, const clk_buffer* norm,
+                              const clk_buffer* residual, const clk_buffer* out, float eps,
+                              int32_t has_residual) {
+    const clk_buffer* bufs[] = {lhs, t, bias, norm, residual, out};
+    const int types[] = {CLK_F16, CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16};
+    if (int st = check_types("opm_update", bufs, types, 6)) return st;
+    if (lhs->rank != 2 || t->rank != 3 || t->dims[0] != lhs->dims[1]) {
+        return invalid("opm_update: lhs must be [B,K] and t [K,D,F]");
+    }
+    const int64_t B = lhs->dims[0], K = lhs->dims[1], D = t->dims[1], F = t->dims[2];
+    if (K % 32 || !opm_width(F) || D > 65535) {
+        return invalid("opm_update: K must be a multiple of 32, F 16, 32, 64 or 128, D at most 65535");
+    }
+    if (elements(bias) != F || elements(norm) != B * D || elements(out) != B * D * F ||
+        (has_residual && elements(residual) != B * D * F)) {
+        return invalid("opm_update: shapes do not match");
+    }
+    if (B == 0 || D == 0) return ok();
+    if (!aligned16(lhs->data) || !aligned16(t->data) || !aligned16(out->data) ||
+        (has_residual && !aligned16(residual->data))) {
+        return invalid("opm_update: lhs, t, residual and out must be 16-byte aligned");
+    }
+    if ((B + kUpBM - 1) / kUpBM > 65535 || K > INT32_MAX) return invalid("opm_update: too large");
+    OpmUpdateArgs a{static_cast<const half_t*>(lhs->data), static_cast<const half_t*>(t->data),
+                    has_residual ? static_cast<const half_t*>(residual->data) : nullptr,
+                    static_cast<const float*>(bias->data), static_cast<const float*>(norm->data),
+                    static_cast<half_t*>(out->data), (int)B, (int)K, (int)D, (int)F, eps};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)((D * F + kUpBN - 1) / kUpBN), (unsigned)((B + kUpBM - 1) / kUpBM));
+    stage_mark(s, 0);
+    hipLaunchKernelGGL(opm_update_kernel, grid, dim3(256), 0, s, a);
+    stage_mark(s, 1);
+    return launch_status("opm_update");
+}
+
+extern "C" int clk_opm_outer(clk_stream stream, const clk_buffer* left, const clk_buffer* right,
+                             const clk_buffer* wT, const clk_buffer* out) {
+    const clk_buffer* bufs[] = {left, right, wT, out};
+    const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    if (int st = check_types("opm_outer", bufs, types, 4)) return st;
+    if (left->rank != 3 || right->rank != 3 || wT->rank != 2 || left->dims[0] != kOpmRows ||
+        right->dims[0] != kOpmRows) {
+        return invalid("opm_outer: left must be [16,B,C], right [16,D,E], wT [F,C*E]");
+    }
+    const int64_t B = left->dims[1], C = left->dims[2], D = right->dims[1], E = right->dims[2];
+    const int64_t F = wT->dims[0];
+    if (C % kOpmChunk || E != kOpmE || D % kOpmD || D / kOpmD > 65535 || wT->dims[1] != C * E ||
+        !opm_width(F)) {
+        return invalid("opm_outer: C a multiple of 16, E 32, D a multiple of 4, F 16, 32, 64 or 128");
+    }
+    if (elements(out) != B * D * F) return invalid("opm_outer: shapes do not match");
+    if (B == 0 || D == 0 || C == 0) return ok();
+    if (!aligned16(left->data) || !aligned16(wT->data) || !aligned16(out->data)) {
+        return invalid("opm_outer: left, wT and out must be 16-byte aligned");
+    }
+    if (B > INT32_MAX || C > INT32_MAX) return invalid("opm_outer: too large");
+    OpmOuterArgs a{static_cast<const half_t*>(left->data), static_cast<const half_t*>(right->data),
+                   static_cast<const half_t*>(wT->data), static_cast<half_t*>(out->data), (int)B,
+                   (int)C, (int)D};
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)((B + kOpmB - 1) / kOpmB), (unsigned)(D / kOpmD));
+    stage_mark(s, 0);
+    switch (F) {
+    case 16: hipLaunchKernelGGL(opm_outer_kernel<16>, grid, dim3(256), 0, s, a); break;
+    case 32: hipLaunchKernelGGL(opm_outer_kernel<32>, grid, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL(opm_outer_kernel<64>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(opm_outer_kernel<128>, grid, dim3(256), 0, s, a); break;
+    }
+    stage_mark(s, 1);
+    return launch_status("opm_outer");
+}

@@ -353,4 +353,28 @@ XLA_FFI_Error* VoltaGdp(XLA_FFI_CallFrame* cf) {
                                         &b[5], &b[6], activation));
 }
 
+XLA_FFI_Error* VoltaOpmUpdate(XLA_FFI_CallFrame* cf) {
+    if (preamble(cf, kCmdBuffer)) return nullptr;
+    Frame f(cf);
+    clk_buffer b[6];
+    float eps;
+    int32_t has_residual;
+    if (!f.buffers(5, 1, b) || !f.f32("eps", &eps) || !f.flag("has_residual", &has_residual)) {
+        return f.decode_error();
+    }
+    clk_stream s;
+    if (!f.stream(&s)) return f.pending();
+    return f.status(clk_opm_update(s, &b[0], &b[1], &b[2], &b[3], &b[4], &b[5], eps, has_residual));
+}
+
+XLA_FFI_Error* VoltaOpmOuter(XLA_FFI_CallFrame* cf) {
+    if (preamble(cf, kCmdBuffer)) return nullptr;
+    Frame f(cf);
+    clk_buffer b[4];
+    if (!f.buffers(3, 1, b)) return f.decode_error();
+    clk_stream s;
+    if (!f.stream(&s)) return f.pending();
+    return f.status(clk_opm_outer(s, &b[0], &b[1], &b[2], &b[3]));
+}
+
 }  // extern "C"

@@ -157,6 +157,24 @@ int clk_gated_dual_proj(clk_stream stream, int32_t device, const clk_buffer* x,
                         const clk_buffer* bg, const clk_buffer* mask, const clk_buffer* out,
                         int64_t activation);
 
+/* ---- outer product mean (reference cuda/volta_ops.cu) ---------------------------------- */
+
+/* VoltaOpmUpdate (volta_ops.cu:643-704, handler cuda/volta_fused_ffi.h:261-297, 420-431):
+ * out[b,d,:] = fp16((lhs[b] @ t[:,d,:] + bias) / (eps + norm[b,d]) [+ residual[b,d,:]]), fp32
+ * accumulation. lhs [B,K], t [K,D,F], residual [B,D,F] F16 (read only with has_residual; may
+ * alias out); bias [F], norm [B,D] F32; out [B,D,F] F16. K a multiple of 32, F in
+ * {16,32,64,128}, D at most 65535. */
+int clk_opm_update(clk_stream stream, const clk_buffer* lhs, const clk_buffer* t,
+                   const clk_buffer* bias, const clk_buffer* norm, const clk_buffer* residual,
+                   const clk_buffer* out, float eps, int32_t has_residual);
+
+/* VoltaOpmOuter (volta_ops.cu:706-792, handler volta_fused_ffi.h:299-335, 433-440):
+ * out[b,d,f] = fp16(sum_c sum_e fp16(sum_a left[a,b,c] right[a,d,e]) wT[f, c E + e]) over the
+ * 16 rows a. left [16,B,C], right [16,D,E=32], wT [F,C*E], out [B,D,F], all F16. C a multiple of
+ * 16, D a multiple of 4 (D/4 at most 65535), F in {16,32,64,128}. */
+int clk_opm_outer(clk_stream stream, const clk_buffer* left, const clk_buffer* right,
+                  const clk_buffer* wT, const clk_buffer* out);
+
 #ifdef __cplusplus
 }
 #endif

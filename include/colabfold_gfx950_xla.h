@@ -61,6 +61,14 @@ struct XLA_FFI_Error* VoltaLayerNorm(struct XLA_FFI_CallFrame* call_frame);
  * attr activation i64. Command-buffer compatible. */
 struct XLA_FFI_Error* VoltaGdp(struct XLA_FFI_CallFrame* call_frame);
 
+/* cuda/volta_fused_ffi.h:420-431. ctx stream; args lhs, t F16, bias, norm F32, residual F16;
+ * ret out F16; attrs eps f32, has_residual bool. Command-buffer compatible. */
+struct XLA_FFI_Error* VoltaOpmUpdate(struct XLA_FFI_CallFrame* call_frame);
+
+/* volta_fused_ffi.h:433-440. ctx stream; args left, right, wT F16; ret out F16.
+ * Command-buffer compatible. */
+struct XLA_FFI_Error* VoltaOpmOuter(struct XLA_FFI_CallFrame* call_frame);
+
 #ifdef __cplusplus
 }
 #endif

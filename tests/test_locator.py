@@ -7,11 +7,13 @@ import pytest
 import colabfold_legacy_kernels as clk
 
 BUILT = ("attention", "attention_bwd", "layer_norm", "gated_dual_proj", "ln_gated_dual_proj",
-         "trimul_epilogue", "ln_projection", "output_projection", "transition")
+         "trimul_epilogue", "ln_projection", "output_projection", "transition", "opm_update",
+         "opm_outer")
 SYMBOLS = {"attention": "VoltaMma", "attention_bwd": "VoltaMmaBwd", "layer_norm": "VoltaLayerNorm",
            "gated_dual_proj": "VoltaGdp", "ln_gated_dual_proj": "VoltaLnGdp",
            "trimul_epilogue": "VoltaTrimulEpilogue", "ln_projection": "VoltaLnProj",
-           "output_projection": "VoltaOutProj", "transition": "VoltaTransition"}
+           "output_projection": "VoltaOutProj", "transition": "VoltaTransition",
+           "opm_update": "VoltaOpmUpdate", "opm_outer": "VoltaOpmOuter"}
 
 
 def test_kernel_names_match_the_reference():
@@ -37,7 +39,8 @@ def test_errors_as_the_reference():
     with pytest.raises(FileNotFoundError):
         clk.library_path("attention", 75)      # a capability this package does not hold
     with pytest.raises(FileNotFoundError):
-        clk.symbol("opm_outer", 950)           # not built for gfx950
+        clk.symbol("opm_outer", 75)            # no row for that capability
+    assert clk.available(950)                  # every kernel of the table is built
     assert not clk.available(70)
     assert not clk.available(950, "no_such_kernel")
     assert clk.kernel_dir(950).endswith(os.path.join("kernels", "gfx950"))

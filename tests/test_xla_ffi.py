@@ -13,7 +13,7 @@ import ffi_frames as ff
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HANDLERS = ("VoltaMma", "VoltaMmaPacked", "VoltaMmaPackedTrim", "VoltaMmaBwd", "VoltaLnGdp",
             "VoltaTrimulEpilogue", "VoltaLnProj", "VoltaOutProj", "VoltaTransition",
-            "VoltaLayerNorm", "VoltaGdp")
+            "VoltaLayerNorm", "VoltaGdp", "VoltaOpmUpdate", "VoltaOpmOuter")
 FAKE = 0x100000  # never dereferenced
 
 
@@ -157,3 +157,43 @@ def test_plain_ops_validation_through_handlers(lib):
     # an empty batch succeeds without a launch
     args = [(ff.F16, FAKE, (0, 64)), (ff.F32, FAKE, (64,)), (ff.F32, FAKE, (64,))]
     assert mock.call(lib.VoltaLayerNorm, args, [(ff.F16, FAKE, (0, 64))], {"eps": (ff.F32, 1e-5)}) is None
+
+
+def test_opm_validation_through_handlers(lib):
+    """The reference's messages (cuda/volta_fused_ffi.h:266-283, 304-318)."""
+    mock = ff.MockXla()
+    up_attrs = {"eps": (ff.F32, 1e-3), "has_residual": (ff.PRED, 0)}
+    one = (ff.F16, FAKE, (1,))
+
+    def up(b, k, d, f, t_k=None, norm=None, res=one, attrs=up_attrs):
+        args = [(ff.F16, FAKE, (b, k)), (ff.F16, FAKE, (k if t_k is None else t_k, d, f)),
+                (ff.F32, FAKE, (f,)), (ff.F32, FAKE, norm or (b, d)), res]
+        return mock.call(lib.VoltaOpmUpdate, args, [(ff.F16, FAKE, (b, d, f))], attrs)
+
+    assert up(4, 64, 8, 128, t_k=32) is not None
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT, "opm_update: lhs must be [B,K] and t [K,D,F]")
+    bad_shape = "opm_update: K must be a multiple of 32, F 16, 32, 64 or 128, D at most 65535"
+    for b, k, d, f in ((4, 48, 8, 128), (4, 64, 8, 96), (4, 64, 65536, 16)):
+        assert up(b, k, d, f) is not None
+        assert mock.errors[-1] == (ff.INVALID_ARGUMENT, bad_shape)
+    assert up(4, 64, 8, 128, norm=(4, 9)) is not None
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT, "opm_update: shapes do not match")
+    attrs = dict(up_attrs, has_residual=(ff.PRED, 1))
+    assert up(4, 64, 8, 128, attrs=attrs) is not None  # a one-element residual with has_residual
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT, "opm_update: shapes do not match")
+    assert up(0, 64, 8, 128) is None  # B == 0: nothing to do
+
+    def outer(rows, b, c, d, e, f, wk=None):
+        args = [(ff.F16, FAKE, (rows, b, c)), (ff.F16, FAKE, (rows, d, e)),
+                (ff.F16, FAKE, (f, c * e if wk is None else wk))]
+        return mock.call(lib.VoltaOpmOuter, args, [(ff.F16, FAKE, (b, d, f))], {})
+
+    assert outer(32, 8, 32, 8, 32, 128) is not None
+    assert mock.errors[-1] == (ff.INVALID_ARGUMENT,
+                               "opm_outer: left must be [16,B,C], right [16,D,E], wT [F,C*E]")
+    bad_shape = "opm_outer: C a multiple of 16, E 32, D a multiple of 4, F 16, 32, 64 or 128"
+    for c, d, e, f, wk in ((24, 8, 32, 128, None), (32, 8, 16, 128, None), (32, 6, 32, 128, None),
+                           (32, 8, 32, 96, None), (32, 8, 32, 128, 512)):
+        assert outer(16, 8, c, d, e, f, wk) is not None
+        assert mock.errors[-1] == (ff.INVALID_ARGUMENT, bad_shape)
+    assert outer(16, 0, 32, 8, 32, 128) is None  # B == 0: nothing to do

@@ -171,3 +171,27 @@ def test_plain_handlers(hip):
                       {"activation": (ff.S64, act)}) is None
         assert same(out, ref)
     assert not m.errors
+
+
+def test_opm_handlers(hip):
+    torch.manual_seed(4)
+    lib = hip.lib()
+    B, K, D, F, C = 37, 64, 64, 128, 32
+    lhs, t = g(B, K), g(K, D, F, s=K ** -.5)
+    bias = g(F, s=.1, dtype=torch.float32)
+    norm = torch.randint(1, 3, (B, D), device="cuda").float()
+    res = g(B, D, F)
+    m = mock()
+    for residual in (None, res):
+        ref = hip.opm_update(lhs, t, bias, norm, residual, eps=1e-3)
+        out = torch.empty_like(ref)
+        rarg = residual if residual is not None else torch.zeros(1, dtype=torch.float16, device="cuda")
+        assert m.call(lib.VoltaOpmUpdate, [b(x) for x in (lhs, t, bias, norm, rarg)], [b(out)],
+                      {"eps": (ff.F32, 1e-3), "has_residual": (ff.PRED, int(residual is not None))}) is None
+        assert same(out, ref)
+    left, right, wT = g(16, B, C), g(16, D, 32), g(F, 32 * C, s=1 / 32)
+    ref = hip.opm_outer(left, right, wT)
+    out = torch.empty_like(ref)
+    assert m.call(lib.VoltaOpmOuter, [b(left), b(right), b(wT)], [b(out)], {}) is None
+    assert same(out, ref)
+    assert not m.errors
