@@ -16,8 +16,10 @@ on its launch stream at its kernel boundaries (clk_set_stage_events); the roofli
 dominant kernel's, its "traffic" the HBM bytes per dispatch that the committed rocprofv3 counter
 summary (profiles/attention_c3_traffic.txt) measured for that kernel. Reported beside the step:
 the gated packed forward VoltaMmaPacked (G = 4) on the same shape, and the fused pair-stack ops
-of config C4 (M = 262144 rows, c = 64 and 128), each timed over enough rotating buffer sets that
-no call finds its inputs in the 256 MB Infinity Cache. cpu_baseline is the fp32 torch-CPU
+of config C4 (M = 262144 rows, c = 64 and 128), the unfused LayerNorm and gated dual projection
+at c = 128 on the same rows, and the outer product mean pair on C3's residues (B = D = 384, 16 MSA
+rows of 32 channels, F = 128), each timed over enough rotating buffer sets that no call finds its
+inputs in the 256 MB Infinity Cache. cpu_baseline is the fp32 torch-CPU
 restatement of the reference tests' jnp attention (oracle/cpu_ref.py; jax is not installed) on a
 bounded row sample of the same workload, on this box's host cores.
 
@@ -276,6 +278,68 @@ def make_fused(torch, hip, op, c, M, g):
     raise KeyError(op)
 
 
+# the reference's unfused ops and the outer product mean, on C4's pair (M = 262144 rows, c = 128)
+# and on C3's residues (B = D = 384) with 16 MSA rows of 32 channels (K = 512), F = 128
+OPM_B = OPM_D = 384
+OPM_ROWS, OPM_C, OPM_F = 16, 32, 128
+NEXT_CASES = ("layer_norm_c128", "gated_dual_proj_c128", "opm_update_f128", "opm_outer_f128")
+
+
+def make_next(torch, hip, name, g):
+    """Inputs and the call for one op of NEXT_CASES, with its algorithmic bytes and flops."""
+    def h(*shape, s=1.0):
+        return (torch.randn(shape, generator=g, device="cuda") * s).half()
+
+    def f(*shape, s=1.0, mean=0.0):
+        return torch.randn(shape, generator=g, device="cuda") * s + mean
+
+    M, c = 262144, 128
+    if name == "layer_norm_c128":
+        x, sc, of = h(M, c), f(c, s=.1, mean=1.), f(c, s=.1)
+        out = torch.empty_like(x)
+        return lambda: hip.layer_norm(x, sc, of, 1e-5, out=out), 4.0 * M * c, 0.0
+    if name == "gated_dual_proj_c128":
+        n = 2 * c
+        x, wp, wg, bp, bg = h(M, c), h(c, n, s=c ** -.5), h(c, n, s=c ** -.5), h(n, s=.1), h(n, s=.1)
+        mask = torch.ones(M, dtype=torch.float16, device="cuda")
+        out = torch.empty((M, n), dtype=torch.float16, device="cuda")
+        return (lambda: hip.gated_dual_proj(x, wp, bp, wg, bg, mask, 0, out=out),
+                2.0 * (M * c + M + M * n), 2.0 * M * c * 2 * n)
+    B, D, K, F = OPM_B, OPM_D, OPM_ROWS * OPM_C, OPM_F
+    if name == "opm_update_f128":
+        lhs, t, bias = h(B, K), h(K, D, F, s=K ** -.5), f(F, s=.1)
+        norm = torch.full((B, D), float(OPM_ROWS), device="cuda")
+        res = h(B, D, F)
+        out = torch.empty_like(res)
+        byts = 2.0 * (B * K + K * D * F + 2 * B * D * F) + 4.0 * (F + B * D)
+        return (lambda: hip.opm_update(lhs, t, bias, norm, res, eps=1e-3, out=out), byts,
+                2.0 * B * D * F * K)
+    if name == "opm_outer_f128":
+        left, right, wT = h(OPM_ROWS, B, OPM_C), h(OPM_ROWS, D, 32), h(F, 32 * OPM_C, s=1 / 32)
+        out = torch.empty((B, D, F), dtype=torch.float16, device="cuda")
+        byts = 2.0 * (OPM_ROWS * (B * OPM_C + D * 32) + F * 32 * OPM_C + B * D * F)
+        flops = 2.0 * B * D * OPM_C * 32 * (OPM_ROWS + F)
+        return lambda: hip.opm_outer(left, right, wT, out=out), byts, flops
+    raise KeyError(name)
+
+
+def time_calls(torch, hip, ev, calls, iters, warmup):
+    """Per-call device time (ms) of rotating calls, from the library's stage events."""
+    for i in range(warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    evs = [ev.create(2) for _ in range(iters)]
+    for i in range(iters):
+        arm(hip, evs[i])
+        calls[i % len(calls)]()
+    disarm(hip)
+    torch.cuda.synchronize()
+    ms = [ev.elapsed_ms(e[0], e[1]) for e in evs]
+    for e in evs:
+        ev.destroy(e)
+    return ms
+
+
 def bench_fused(torch, hip, ev, iters, warmup):
     M = 262144
     g = torch.Generator(device="cuda")
@@ -285,21 +349,18 @@ def bench_fused(torch, hip, ev, iters, warmup):
         byts, flops = fused_bytes_flops(op, M, c, n=512 if op == "ln_projection" else 128,
                                         heads=4 if op == "ln_projection" else 0)
         nsets = max(3, math.ceil(3 * MALL_BYTES / byts))
-        calls = [make_fused(torch, hip, op, c, M, g) for _ in range(nsets)]
-        for i in range(warmup):
-            calls[i % nsets][0]()
-        torch.cuda.synchronize()
-        evs = [ev.create(2) for _ in range(iters)]
-        for i in range(iters):
-            arm(hip, evs[i])
-            calls[i % nsets][0]()
-        disarm(hip)
-        torch.cuda.synchronize()
-        ms = [ev.elapsed_ms(e[0], e[1]) for e in evs]
-        for e in evs:
-            ev.destroy(e)
+        calls = [make_fused(torch, hip, op, c, M, g)[0] for _ in range(nsets)]
+        ms = time_calls(torch, hip, ev, calls, iters, warmup)
         res["%s_c%d" % (op, c)] = roof_entry(ms, flops, byts, buffer_sets=nsets)
         del calls
+        torch.cuda.empty_cache()
+    for name in NEXT_CASES:
+        first = make_next(torch, hip, name, g)
+        nsets = max(3, math.ceil(3 * MALL_BYTES / first[1]))
+        calls = [first[0]] + [make_next(torch, hip, name, g)[0] for _ in range(nsets - 1)]
+        ms = time_calls(torch, hip, ev, calls, iters, warmup)
+        res[name] = roof_entry(ms, first[2], first[1], buffer_sets=nsets)
+        del calls, first
         torch.cuda.empty_cache()
     return res
 

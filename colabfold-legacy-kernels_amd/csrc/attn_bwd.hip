@@ -38,9 +38,10 @@ struct BwdArgs {
     half_t* dk;
     half_t* dv;
     float* dbias;
-    float* delta;    // workspace [N, H, SqA]: rowsum(out * dout), 0 past Sq
-    float* lse2p;    // workspace [N, H, SqA]: lse, +inf past Sq
-    float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside
+    float* delta;    // workspace [N, H, SqA]: -rowsum(out * dout), 0 past Sq
+    float* lse2p;    // workspace [N, H, SqA]: -lse / c1, -inf past Sq
+    float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside; then one row
+                     // of the masked logit times log2e and one row of zeros, [SqA] each
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
     int N, H, Sq, Sk, D;
     int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
@@ -48,6 +49,8 @@ struct BwdArgs {
     int chunk;       // batch rows per dkdv workgroup
     int chunks;
     float scale;
+    float c1;    // scale log2e, or 1 where |scale log2e| is below 1e-30
+    int kscale;  // 0 where c1 stands in for a negligible scale: the dK/dV kernel's K is then zero
     int bias_vec, mask_vec;
 };
 
@@ -143,8 +146,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
         // a query past Sq gets lse2 = +inf, so its p is 0 whatever its logits
         lse2[qb] = in ? a.lse[nh * a.Sq + gq] : INFINITY;
         if (gq < a.SqA && g == 0) {
-            a.delta[nh * a.SqA + gq] = in ? dlt[qb] : 0.f;
-            a.lse2p[nh * a.SqA + gq] = lse2[qb];
+            // the dK/dV kernel's accumulator inputs: -delta and -lse2 / c1 (past Sq the latter
+            // is infinite with the sign that makes c1 times it -inf)
+            a.delta[nh * a.SqA + gq] = in ? -dlt[qb] : 0.f;
+            a.lse2p[nh * a.SqA + gq] = (in ? -lse2[qb] : -INFINITY) / a.c1;
         }
     }
 
@@ -305,10 +310,16 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
 //
 // A workgroup owns 64 keys (four key groups of 16, one wave each) and QG query groups: for each
 // batch row n of its chunk, query group qg takes query tiles qg, qg + QG, ... of 32 queries,
-// staged by its four waves into its own LDS buffers. Every dBias element (key, q) therefore has
-// one owner wave, which adds its dS in a fixed order; the query groups' dK / dV partials are
-// summed in group order through LDS at the end of each row. Loads run one tile (and K/V one row)
-// ahead of their use.
+// staged by its four waves into its own pair of LDS buffers (one read, one being written, one
+// barrier per tile). Every dBias element (key, q) therefore has one owner wave, which adds its dS
+// in a fixed order; the query groups' dK / dV partials are summed in group order through LDS at
+// the end of each row.
+//
+// The per-query terms enter the MFMAs as accumulator inputs: S starts from -lse2 / (scale log2e)
+// and dP from -delta (both staged in LDS with the tile), so that s2 = scale log2e S + bias log2e
+// is one fma and dS = p dP one multiply. A dead key (masked, or past Sk) has zero K and V rows and
+// reads the masked-logit row in place of its bias, so p still carries dV; its dS is set to 0 in a
+// path that only waves holding a dead key take.
 // ------------------------------------------------------------------------------------------
 template <int DP, int QG>
 struct DkdvTile {
@@ -319,11 +330,13 @@ struct DkdvTile {
     static constexpr int kLd = DP + 8;
     static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO chunks of one tile
     static constexpr int kCPT = (kChunks + 255) / 256;
-    static constexpr int kStage = 2 * kBQ * kLd;      // halfs per query group: Q and dO rows
+    // halfs per query group and buffer: Q and dO rows, then the tile's -lse2 / c1 and -delta
+    static constexpr int kRowsHalfs = 2 * kBQ * kLd;
+    static constexpr int kStage = kRowsHalfs + 2 * kBQ * 2;
     static constexpr int kCombineBytes = 4 * (QG - 1) * kDB * kWave * 4 * 4;
-    // the staging area, which the end-of-row combine of the query groups reuses
+    // two staging buffers per query group; the end-of-row combine of the groups reuses the area
     static constexpr int kStageBytes =
-        kStage * 2 * QG > kCombineBytes ? kStage * 2 * QG : kCombineBytes;
+        kStage * 2 * 2 * QG > kCombineBytes ? kStage * 2 * 2 * QG : kCombineBytes;
     // dBias partial [kBK keys][SqA + kDBPad]: the pad staggers the keys' rows across LDS banks
     static constexpr int kDBPad = 4;
 };
@@ -348,8 +361,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int IT = (qtiles + QG - 1) / QG;
     const int total = (n_end - n_begin) * IT;
 
-    half_t* Qs = reinterpret_cast<half_t*>(lds_raw) + qg * T::kStage;
-    half_t* Os = Qs + T::kBQ * T::kLd;
+    half_t* const stage0 = reinterpret_cast<half_t*>(lds_raw) + qg * T::kStage;
+    constexpr int kBufStride = QG * T::kStage;  // halfs from buffer 0 to buffer 1 of a group
     const int dbld = a.SqA + T::kDBPad;
     float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][dbld]
     float* comb = reinterpret_cast<float*>(lds_raw);                   // between rows only
@@ -359,17 +372,22 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 
     const float scale = a.scale;
-    const float scale_log2e = a.scale * kLog2e;
-    const float* bias_row = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
+    const float c1 = a.c1;  // scale log2e, or 1 where that is below fp32 resolution (K is zero then)
+    const int64_t rows_h = (int64_t)a.H * a.SkA * a.SqA;
+    const float* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
+    const float* bt_dead = a.biast + rows_h + 8 * g;  // the masked logit times log2e
 
-    // the next tile of this query group: Q / dO chunks to stage, and this lane's eight queries'
-    // lse2, delta and log2e-scaled bias at its key (padded past Sq: lse2 +inf, delta 0)
+    // the next tile of this query group: Q / dO chunks and the tile's -lse2 / c1 and -delta
+    // (threads 0..15, one float4 each) to stage, fetched early in a tile; this lane's eight
+    // queries' log2e-scaled bias at its key, fetched once the current ones are consumed (padded
+    // past Sq: -lse2 / c1 infinite, -delta 0, bias 0)
     struct Pre {
         half8 s[T::kCPT];
-        float l2[8], dl[8], bt[8];
+        float4v st;
+        float4v bt[2];
     };
     Pre pre;
-    const auto fetch = [&](Pre& d, int n, int it) {
+    const auto fetch_s = [&](Pre& d, int n, int it) {
         const int qi = it * QG + qg, q0 = qi * T::kBQ;
         const bool valid = qi < qtiles;
         const int64_t nh = (int64_t)n * a.H + h, base = nh * a.Sq * a.D;
@@ -382,24 +400,22 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             const half_t* src = which ? a.dout : a.q;
             d.s[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
         }
-        if (valid) {
-            const float* l2p = a.lse2p + nh * a.SqA + q0 + 8 * g;
-            const float* dlp = a.delta + nh * a.SqA + q0 + 8 * g;
-            const float4 l2a = *reinterpret_cast<const float4*>(l2p);
-            const float4 l2b = *reinterpret_cast<const float4*>(l2p + 4);
-            const float4 dla = *reinterpret_cast<const float4*>(dlp);
-            const float4 dlb = *reinterpret_cast<const float4*>(dlp + 4);
-            const float4 bta = *reinterpret_cast<const float4*>(bias_row + q0);
-            const float4 btb = *reinterpret_cast<const float4*>(bias_row + q0 + 4);
-            d.l2[0] = l2a.x; d.l2[1] = l2a.y; d.l2[2] = l2a.z; d.l2[3] = l2a.w;
-            d.l2[4] = l2b.x; d.l2[5] = l2b.y; d.l2[6] = l2b.z; d.l2[7] = l2b.w;
-            d.dl[0] = dla.x; d.dl[1] = dla.y; d.dl[2] = dla.z; d.dl[3] = dla.w;
-            d.dl[4] = dlb.x; d.dl[5] = dlb.y; d.dl[6] = dlb.z; d.dl[7] = dlb.w;
-            d.bt[0] = bta.x; d.bt[1] = bta.y; d.bt[2] = bta.z; d.bt[3] = bta.w;
-            d.bt[4] = btb.x; d.bt[5] = btb.y; d.bt[6] = btb.z; d.bt[7] = btb.w;
+        if (valid && gtid < 16) {
+            const float* src = (gtid < 8 ? a.lse2p : a.delta) + nh * a.SqA + q0 + 4 * (gtid & 7);
+            d.st = *reinterpret_cast<const float4v*>(src);
         }
     };
-    const auto stage_tile = [&](const Pre& c) {
+    const auto fetch_c = [&](Pre& d, int it, bool alive) {
+        const int qi = it * QG + qg, q0 = qi * T::kBQ;
+        if (qi < qtiles) {
+            const float* btp = (alive ? bt_own : bt_dead) + q0;
+            d.bt[0] = *reinterpret_cast<const float4v*>(btp);
+            d.bt[1] = *reinterpret_cast<const float4v*>(btp + 4);
+        }
+    };
+    const auto stage_tile = [&](const Pre& d, int buf) {
+        half_t* Qs = stage0 + buf * kBufStride;
+        half_t* Os = Qs + T::kBQ * T::kLd;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
             const int cc = gtid + i * 256;
@@ -407,36 +423,44 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
                 const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
                 half_t* rm = which ? Os : Qs;
-                *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = c.s[i];
+                *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = d.s[i];
             }
+        }
+        if (gtid < 16) {
+            // [-lse2 / c1 of the 32 queries][-delta of the 32 queries]
+            *reinterpret_cast<float4v*>(reinterpret_cast<float*>(Qs + T::kRowsHalfs) + 4 * gtid) = d.st;
         }
     };
 
-    // K and V of a row as the B operands (lane column = key, slots d = 32 ks + 8 g + j)
+    // K and V of a row as the B operands (lane column = key, slots d = 32 ks + 8 g + j), both zero
+    // for a dead key
     half8 kopn[T::kKS], vopn[T::kKS];
-    bool kaliven = false;
-    // a masked key's K is zero, so its score is 0 and its logit the masked logit (its bias below)
+    bool aliven = false;
     const auto fetch_kv = [&](int n) {
         const int64_t kbase = ((int64_t)n * a.H + h) * a.Sk * a.D;
-        kaliven = kin && a.kmask[(int64_t)n * a.Sk + key] != 0;
+        aliven = kin && a.kmask[(int64_t)n * a.Sk + key] != 0;
 #pragma unroll
         for (int ks = 0; ks < T::kKS; ++ks) {
             const int d0 = 32 * ks + 8 * g;
-            const bool ok = kin && d0 < a.D;
-            kopn[ks] = ok && kaliven ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
+            const bool ok = aliven && d0 < a.D;
+            kopn[ks] = ok && a.kscale ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
             vopn[ks] = ok ? bld8(a.v + kbase + (int64_t)key * a.D + d0) : bzero8();
         }
     };
 
     half8 kop[T::kKS], vop[T::kKS];
-    bool kalive = false;
+    bool alive = false, all_alive = true;
     float4v accv[T::kDB], acck[T::kDB];
 
     if (total > 0) {
-        fetch(pre, n_begin, 0);
         fetch_kv(n_begin);
+        fetch_s(pre, n_begin, 0);
+        fetch_c(pre, 0, aliven);
+        stage_tile(pre, 0);
     }
+    __syncthreads();
     for (int t = 0, it = 0, n = n_begin; t < total; ++t) {
+        const int buf = t & 1;
         const int qi = it * QG + qg, q0 = qi * T::kBQ;
         const bool valid = qi < qtiles;
         if (it == 0) {
@@ -445,7 +469,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 kop[ks] = kopn[ks];
                 vop[ks] = vopn[ks];
             }
-            kalive = kaliven;
+            alive = aliven;
+            all_alive = __all(alive);
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
                 accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -453,68 +478,50 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             }
             if (n + 1 < n_end) fetch_kv(n + 1);
         }
+        const half_t* Qs = stage0 + buf * kBufStride;
+        const half_t* Os = Qs + T::kBQ * T::kLd;
+        const float* Ls = reinterpret_cast<const float*>(Qs + T::kRowsHalfs);  // -lse2 / c1, -delta
+        const bool wrap = it + 1 == IT;
+        const int n_next = wrap ? n + 1 : n, it_next = wrap ? 0 : it + 1;
+        if (t + 1 < total) fetch_s(pre, n_next, it_next);
 
-        __syncthreads();  // this group's previous tile (and the last row's combine) are done
-        stage_tile(pre);
-        // p = exp2(s scale log2e + bl), bl = (bias or the masked logit) log2e - lse2, formed
-        // here (pinned) so the next fetch may overwrite the prefetched values without copies
-        float bl[8], dl[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            bl[j] = pin_f32((kalive ? pre.bt[j] : kMaskedLogit * kLog2e) - pre.l2[j]);
-            dl[j] = pre.dl[j];
-        }
-        __syncthreads();
-        if (t + 1 < total) {
-            const bool wrap = it + 1 == IT;
-            fetch(pre, wrap ? n + 1 : n, wrap ? 0 : it + 1);
-        }
-
+        // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
+        // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
+        float x[8];
+        float4v dp[2];
         if (valid) {
-            // S and dP: A row r of query block qb is query 8 (r/4) + 4 qb + r%4 of the tile
-            float4v s[2], dp[2];
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                const int qrow = 16 * qb + r16;  // query 8 (r/4) + 4 qb + r%4
-                s[qb] = float4v{0.f, 0.f, 0.f, 0.f};
-                dp[qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                const int qrow = 16 * qb + r16;
+                float4v s = *reinterpret_cast<const float4v*>(Ls + 8 * g + 4 * qb);
+                dp[qb] = *reinterpret_cast<const float4v*>(Ls + T::kBQ + 8 * g + 4 * qb);
 #pragma unroll
                 for (int ks = 0; ks < T::kKS; ++ks) {
                     const half8 qa = bld8(&Qs[qrow * T::kLd + 32 * ks + 8 * g]);
                     const half8 oa = bld8(&Os[qrow * T::kLd + 32 * ks + 8 * g]);
-                    s[qb] = mfma16x16x32(qa, kop[ks], s[qb]);
+                    s = mfma16x16x32(qa, kop[ks], s);
                     dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
                 }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1, pre.bt[qb][i]);
             }
-
-            // lane holds query q0 + 8 g + 4 qb + i of its key: slot j = 4 qb + i
-            half8 pb, dsb;
+        }
+        half8 pb, dsb;
+        if (valid) {
             float dsf[8];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int j = 4 * qb + i;
-                    const float p = exp2_fast(fmaf(s[qb][i], scale_log2e, bl[j]));
-                    const float ds = pin_f32(kalive ? p * (dp[qb][i] - dl[j]) : 0.f);
-                    pb[j] = (half_t)p;
-                    dsb[j] = (half_t)ds;
-                    dsf[j] = ds;
-                }
+            for (int j = 0; j < 8; ++j) {
+                const float p = exp2_fast(x[j]);
+                dsf[j] = pin_f32(p * dp[j >> 2][j & 3]);
+                pb[j] = (half_t)p;
             }
-
-            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
-            // its k-slots queries 8 g + j, read transposed from the row-major tiles
-            const auto orow = [&](int r) { return Os + perm_row(r, 8) * T::kLd; };
-            const auto qrow = [&](int r) { return Qs + perm_row(r, 8) * T::kLd; };
+            if (!all_alive) {
+                // a dead key's dS is 0 (its p, from the masked logit, still carries dV)
 #pragma unroll
-            for (int db = 0; db < T::kDB; ++db) {
-                const half8 ot = lds_operand_tr(orow, g, r16, 4 * db, DP / 4);
-                const half8 qt = lds_operand_tr(qrow, g, r16, 4 * db, DP / 4);
-                accv[db] = mfma16x16x32(ot, pb, accv[db]);
-                acck[db] = mfma16x16x32(qt, dsb, acck[db]);
+                for (int j = 0; j < 8; ++j) dsf[j] = alive ? dsf[j] : 0.f;
             }
-
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dsb[j] = (half_t)dsf[j];
             if constexpr (DBIAS) {
                 // this lane is the only writer of these eight elements, so the order is fixed
                 // (a read-modify-write: LDS float atomics measured several times slower here)
@@ -527,10 +534,29 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 *reinterpret_cast<float4*>(row + 4) = hi;
             }
         }
+        // the next tile's accumulator inputs and bias, into the registers just consumed
+        if (t + 1 < total) fetch_c(pre, it_next, wrap ? aliven : alive);
+
+        if (valid) {
+
+            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
+            // its k-slots queries 8 g + j, read transposed from the row-major tiles
+            const auto orow = [&](int r) { return Os + perm_row(r, 8) * T::kLd; };
+            const auto qrow = [&](int r) { return Qs + perm_row(r, 8) * T::kLd; };
+#pragma unroll
+            for (int db = 0; db < T::kDB; ++db) {
+                const half8 ot = lds_operand_tr(orow, g, r16, 4 * db, DP / 4);
+                const half8 qt = lds_operand_tr(qrow, g, r16, 4 * db, DP / 4);
+                accv[db] = mfma16x16x32(ot, pb, accv[db]);
+                acck[db] = mfma16x16x32(qt, dsb, acck[db]);
+            }
+        }
 
         if (it == IT - 1) {
             if constexpr (QG > 1) {
-                // the query groups' partials, summed in group order by group 0 (two rounds)
+                // the query groups' partials, summed in group order by group 0 (two rounds); the
+                // staging area is free: every wave is past this tile's reads, and the next tile
+                // is staged below
                 float* slot = comb + ((kg * (QG - 1) + qg - 1) * T::kDB) * 256 + lane * 4;
                 __syncthreads();
                 if (qg > 0) {
@@ -560,6 +586,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                             accv[db] += *reinterpret_cast<const float4v*>(
                                 comb + ((kg * (QG - 1) + o) * T::kDB + db) * 256 + lane * 4);
                 }
+                __syncthreads();
             }
             if (qg == 0 && kin) {
                 // lane holds d = (DP/4) g .. +DP/4 of its key
@@ -579,6 +606,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 }
             }
         }
+        // the other buffer was last read a tile ago, before the barrier that ended that tile
+        if (t + 1 < total) stage_tile(pre, buf ^ 1);
+        __syncthreads();
         if (++it == IT) {
             it = 0;
             ++n;
@@ -586,7 +616,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 
     if constexpr (DBIAS) {
-        __syncthreads();
         float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * T::kBK;
         for (int i = tid; i < a.SqA * T::kBK; i += T::kThreads) {
             dst[i] = DBt[(i % T::kBK) * dbld + i / T::kBK];  // to [SqA][64]
@@ -594,7 +623,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
-// biast[h][key][q] = bias[h][q][key] * log2e for q < Sq, key < Sk, else 0, over [H][SkA][SqA]:
+// biast[h][key][q] = bias[h][q][key] * log2e for q < Sq, key < Sk, else 0, over [H][SkA][SqA],
+// and the two [SqA] rows after it (the masked logit times log2e, zeros):
 // a workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads where the bias
 // rows allow them and 16-byte stores (SqA is a multiple of 32).
 __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
@@ -628,6 +658,12 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
             make_float4(tile[qc][kk], tile[qc + 1][kk], tile[qc + 2][kk], tile[qc + 3][kk]);
         *reinterpret_cast<float4*>(dst + 4) =
             make_float4(tile[qc + 4][kk], tile[qc + 5][kk], tile[qc + 6][kk], tile[qc + 7][kk]);
+    }
+    if (h == 0 && kblk == 0 && tid < 64) {
+        // the two rows after the last head: the masked logit times log2e, then zeros
+        float* extra = a.biast + (int64_t)a.H * a.SkA * a.SqA;
+        if (tid < 32) extra[q0 + tid] = kMaskedLogit * kLog2e;
+        else extra[a.SqA + q0 + tid - 32] = 0.f;
     }
 }
 
@@ -765,7 +801,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
     p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // delta, and lse2 after it
-    p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(float));
+    p.biast_bytes = round256(((size_t)H * p.SkA + 2) * p.SqA * sizeof(float));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     return p;
 }
@@ -903,6 +939,9 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.chunk = p.chunk;
     a.chunks = p.chunks;
     a.scale = scale;
+    a.c1 = scale * kLog2e;
+    a.kscale = fabsf(a.c1) >= 1e-30f;
+    if (!a.kscale) a.c1 = 1.f;  // scale log2e S is below fp32 resolution against the bias
     a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
     a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
