@@ -40,8 +40,7 @@ struct BwdArgs {
     float* dbias;
     float* delta;    // workspace [N, H, SqA]: -rowsum(out * dout), 0 past Sq
     float* lse2p;    // workspace [N, H, SqA]: -lse / c1, -inf past Sq
-    float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside; then one row
-                     // of the masked logit times log2e and one row of zeros, [SqA] each
+    float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
     int N, H, Sq, Sk, D;
     int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
@@ -106,8 +105,9 @@ struct DqTile {
     static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
 };
 
+// At D = 32 three waves per SIMD (at most 168 VGPRs, a few spilled) measured faster than two.
 template <int DP>
-__global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_bwd_dq_kernel(BwdArgs a) {
     using T = DqTile<DP>;
     // two key tiles in flight: one being read by the MFMAs, the next being written
     __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kLd];
@@ -115,8 +115,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
+    // head-major order: an XCD's contiguous run of items covers few heads, so the bias rows
+    // it reads stay in its L2
     const int qt = item % QT, rest = item / QT;
-    const int h = rest % a.H, n = rest / a.H;
+    const int n = rest % a.N, h = rest / a.N;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int64_t nh = (int64_t)n * a.H + h;
@@ -161,9 +163,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
 
     const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
 
-    // K/V chunks one tile ahead; a masked key's K row is staged as zeros (its score is 0)
+    // K/V chunks one tile ahead, with their key's raw mask byte, examined only at the stage a
+    // tile later (so the loads stay in flight); a masked key's K row is staged as zeros
     half8 kreg[T::kCPT], vreg[T::kCPT];
-    bool kkeep[T::kCPT];
+    uint32_t kmb[T::kCPT];
     const auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
             const int64_t off = kbase + (int64_t)(k0 + row) * a.D + col;
             kreg[i] = ok ? bld8(a.k + off) : bzero8();
             vreg[i] = ok ? bld8(a.v + off) : bzero8();
-            kkeep[i] = ok && mrow[k0 + row] != 0;
+            kmb[i] = ok ? (uint32_t)mrow[k0 + row] : 0u;
         }
     };
     const auto stage = [&](int buf) {
@@ -182,7 +185,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
             const int c = tid + i * T::kThreads;
             if (c < T::kChunks) {
                 const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-                const half8 kv = kkeep[i] ? kreg[i] : bzero8();
+                const half8 kv = kmb[i] != 0u ? kreg[i] : bzero8();
                 const int prow = perm_row(row, 16);
                 *reinterpret_cast<half8*>(&Ks2[buf][prow * T::kLd + col]) = kv;
                 *reinterpret_cast<half8*>(&Vs2[buf][prow * T::kLd + col]) = vreg[i];
@@ -193,9 +196,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
     const float scale = a.scale;
     const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
 
-    // bias of this lane's 16 keys k0 + 16 g .. +15, one key tile ahead of its use; a masked key
-    // or a key past Sk gets bias -inf, so its p, and with it its dS, is 0
+    // bias of this lane's 16 keys k0 + 16 g .. +15 and their raw mask bytes, one key tile ahead
+    // of their use; when the tile comes up, a masked key or a key past Sk gets bias -inf, so its
+    // p, and with it its dS, is 0
     BH16 bias_n[T::kQB];
+    uint4 mask_n;
     const auto fetch_bm = [&](int k0) {
         const int kl = k0 + 16 * g;
         const int kvalid = a.Sk - kl;
@@ -205,12 +210,14 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
             const int gqc = gq < a.Sq ? gq : a.Sq - 1;
             bias_n[qb] = bload_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
         }
-        const uint32_t keep = mask_bits16(bload_m16(mrow + kl, kvalid, a.mask_vec), kvalid);
+        mask_n = bload_m16(mrow + kl, kvalid, a.mask_vec);
+    };
+    const auto fix_bias = [&](int k0, BH16 (&b)[T::kQB], uint4 m) {
+        const uint32_t keep = mask_bits16(m, a.Sk - (k0 + 16 * g));
         if (keep != 0xffffu) {
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb)
-                fill_bias16(bias_n[qb].lo, bias_n[qb].hi, keep, 0u, (half_t)(-INFINITY),
-                            (half_t)(-INFINITY));
+                fill_bias16(b[qb].lo, b[qb].hi, keep, 0u, (half_t)(-INFINITY), (half_t)(-INFINITY));
         }
     };
 
@@ -227,10 +234,12 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
         BH16 bias16[T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) bias16[qb] = bias_n[qb];
+        const uint4 mask16 = mask_n;
         if (more) {
             fetch(k0 + T::kBK);
             fetch_bm(k0 + T::kBK);
         }
+        fix_bias(k0, bias16, mask16);
 
 
         float4v s[4][T::kQB], dp[4][T::kQB];
@@ -318,8 +327,8 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads) void attn_bwd_dq_kernel(BwdAr
 // The per-query terms enter the MFMAs as accumulator inputs: S starts from -lse2 / (scale log2e)
 // and dP from -delta (both staged in LDS with the tile), so that s2 = scale log2e S + bias log2e
 // is one fma and dS = p dP one multiply. A dead key (masked, or past Sk) has zero K and V rows and
-// reads the masked-logit row in place of its bias, so p still carries dV; its dS is set to 0 in a
-// path that only waves holding a dead key take.
+// the masked logit in place of its bias, so p still carries dV; its dS is set to 0. Both happen
+// on a path that only waves holding a dead key take.
 // ------------------------------------------------------------------------------------------
 template <int DP, int QG>
 struct DkdvTile {
@@ -347,8 +356,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds_raw[];
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
+    // head-major order, as in the forward: an XCD's run of items reads few heads' bias columns
     const int kblk = item % a.kblocks, rest = item / a.kblocks;
-    const int h = rest % a.H, c = rest / a.H;
+    const int c = rest % a.chunks, h = rest / a.chunks;
     const int n_begin = c * a.chunk;
     const int n_end = min(a.N, n_begin + a.chunk);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -373,9 +383,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     const float scale = a.scale;
     const float c1 = a.c1;  // scale log2e, or 1 where that is below fp32 resolution (K is zero then)
-    const int64_t rows_h = (int64_t)a.H * a.SkA * a.SqA;
     const float* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
-    const float* bt_dead = a.biast + rows_h + 8 * g;  // the masked logit times log2e
+    constexpr float kDead = kMaskedLogit * kLog2e;  // a dead key's bias times log2e
 
     // the next tile of this query group: Q / dO chunks and the tile's -lse2 / c1 and -delta
     // (threads 0..15, one float4 each) to stage, fetched early in a tile; this lane's eight
@@ -405,10 +414,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             d.st = *reinterpret_cast<const float4v*>(src);
         }
     };
-    const auto fetch_c = [&](Pre& d, int it, bool alive) {
+    const auto fetch_c = [&](Pre& d, int it) {
         const int qi = it * QG + qg, q0 = qi * T::kBQ;
         if (qi < qtiles) {
-            const float* btp = (alive ? bt_own : bt_dead) + q0;
+            const float* btp = bt_own + q0;
             d.bt[0] = *reinterpret_cast<const float4v*>(btp);
             d.bt[1] = *reinterpret_cast<const float4v*>(btp + 4);
         }
@@ -432,17 +441,18 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         }
     };
 
-    // K and V of a row as the B operands (lane column = key, slots d = 32 ks + 8 g + j), both zero
-    // for a dead key
+    // K and V of the next row as the B operands (lane column = key, slots d = 32 ks + 8 g + j)
+    // and the key's raw mask byte; both operands become zero for a dead key when the row comes
+    // up, so nothing loaded here is examined before then
     half8 kopn[T::kKS], vopn[T::kKS];
-    bool aliven = false;
+    uint32_t mbn = 0u;
     const auto fetch_kv = [&](int n) {
         const int64_t kbase = ((int64_t)n * a.H + h) * a.Sk * a.D;
-        aliven = kin && a.kmask[(int64_t)n * a.Sk + key] != 0;
+        mbn = kin ? (uint32_t)a.kmask[(int64_t)n * a.Sk + key] : 0u;
 #pragma unroll
         for (int ks = 0; ks < T::kKS; ++ks) {
             const int d0 = 32 * ks + 8 * g;
-            const bool ok = aliven && d0 < a.D;
+            const bool ok = kin && d0 < a.D;
             kopn[ks] = ok && a.kscale ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
             vopn[ks] = ok ? bld8(a.v + kbase + (int64_t)key * a.D + d0) : bzero8();
         }
@@ -455,7 +465,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     if (total > 0) {
         fetch_kv(n_begin);
         fetch_s(pre, n_begin, 0);
-        fetch_c(pre, 0, aliven);
+        fetch_c(pre, 0);
         stage_tile(pre, 0);
     }
     __syncthreads();
@@ -464,12 +474,12 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const int qi = it * QG + qg, q0 = qi * T::kBQ;
         const bool valid = qi < qtiles;
         if (it == 0) {
+            alive = mbn != 0u;
 #pragma unroll
             for (int ks = 0; ks < T::kKS; ++ks) {
-                kop[ks] = kopn[ks];
-                vop[ks] = vopn[ks];
+                kop[ks] = alive ? kopn[ks] : bzero8();
+                vop[ks] = alive ? vopn[ks] : bzero8();
             }
-            alive = aliven;
             all_alive = __all(alive);
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
@@ -502,8 +512,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                     s = mfma16x16x32(qa, kop[ks], s);
                     dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
                 }
+                // a dead key's bias is the masked logit
+                const float4v bt = all_alive || alive ? pre.bt[qb] : float4v{kDead, kDead, kDead, kDead};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1, pre.bt[qb][i]);
+                for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1, bt[i]);
             }
         }
         half8 pb, dsb;
@@ -535,7 +547,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             }
         }
         // the next tile's accumulator inputs and bias, into the registers just consumed
-        if (t + 1 < total) fetch_c(pre, it_next, wrap ? aliven : alive);
+        if (t + 1 < total) fetch_c(pre, it_next);
 
         if (valid) {
 
@@ -623,8 +635,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
-// biast[h][key][q] = bias[h][q][key] * log2e for q < Sq, key < Sk, else 0, over [H][SkA][SqA],
-// and the two [SqA] rows after it (the masked logit times log2e, zeros):
+// biast[h][key][q] = bias[h][q][key] * log2e for q < Sq, key < Sk, else 0, over [H][SkA][SqA]:
 // a workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads where the bias
 // rows allow them and 16-byte stores (SqA is a multiple of 32).
 __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
@@ -658,12 +669,6 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
             make_float4(tile[qc][kk], tile[qc + 1][kk], tile[qc + 2][kk], tile[qc + 3][kk]);
         *reinterpret_cast<float4*>(dst + 4) =
             make_float4(tile[qc + 4][kk], tile[qc + 5][kk], tile[qc + 6][kk], tile[qc + 7][kk]);
-    }
-    if (h == 0 && kblk == 0 && tid < 64) {
-        // the two rows after the last head: the masked logit times log2e, then zeros
-        float* extra = a.biast + (int64_t)a.H * a.SkA * a.SqA;
-        if (tid < 32) extra[q0 + tid] = kMaskedLogit * kLog2e;
-        else extra[a.SqA + q0 + tid - 32] = 0.f;
     }
 }
 
@@ -801,7 +806,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
     p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // delta, and lse2 after it
-    p.biast_bytes = round256(((size_t)H * p.SkA + 2) * p.SqA * sizeof(float));
+    p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(float));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     return p;
 }

@@ -100,8 +100,10 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
+    // head-major order: an XCD's contiguous run of items covers few heads, so the bias rows
+    // it reads stay in its L2
     const int qt = item % QT, rest = item / QT;
-    const int h = rest % a.H, n = rest / a.H;
+    const int n = rest % a.N, h = rest / a.N;
     const int q0 = qt * T::kBQ;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
@@ -152,11 +154,12 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
 
     const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
 
-    // K/V tile chunks held in registers one tile ahead of their LDS store, with their key's mask:
-    // a masked key's K row is staged as zeros, so its score is exactly 0 and its bias register
-    // (which then holds the masked logit) is its logit
+    // K/V tile chunks held in registers one tile ahead of their LDS store, with their key's raw
+    // mask byte: a masked key's K row is staged as zeros, so its score is exactly 0 and its bias
+    // register (which then holds the masked logit) is its logit. Nothing loaded here is examined
+    // before the stage a tile later, so the loads stay in flight meanwhile.
     half8 kreg[T::kCPT], vreg[T::kCPT];
-    bool kkeep[T::kCPT];
+    uint32_t kmb[T::kCPT];
     const auto fetch = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
             const int64_t off = kbase + (int64_t)(k0 + row) * a.ks + col;
             kreg[i] = ok ? ld8(a.k + off) : zero8();
             vreg[i] = ok ? ld8(a.v + off) : zero8();
-            kkeep[i] = ok && mrow[k0 + row] != 0;
+            kmb[i] = ok ? (uint32_t)mrow[k0 + row] : 0u;
         }
     };
     const auto stage = [&](int buf) {
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
             if (c < T::kChunks) {
                 const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
                 *reinterpret_cast<half8*>(&Ks[perm_row(row, 16) * T::kKsLd + col]) =
-                    kkeep[i] ? kreg[i] : zero8();
+                    kmb[i] != 0u ? kreg[i] : zero8();
                 *reinterpret_cast<half8*>(&Vs[row * T::kKsLd + col]) = vreg[i];
             }
         }
@@ -187,9 +190,11 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
     const float scale = a.scale;
     const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
 
-    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, one key tile ahead of its
-    // use; a masked key's bias becomes the masked logit -1e4, a key past Sk's -inf
+    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, and their raw mask bytes,
+    // one key tile ahead of their use; when the tile comes up, a masked key's bias becomes the
+    // masked logit -1e4 and a key past Sk's -inf
     H16 bias_n[T::kQB];
+    uint4 mask_n;
     const auto fetch_bm = [&](int k0) {
         const int kl = k0 + 16 * g;
         const int kvalid = a.Sk - kl;
@@ -199,12 +204,16 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
             const int gqc = gq < a.Sq ? gq : a.Sq - 1;
             bias_n[qb] = load_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
         }
-        const uint32_t keep = mask_bits16(load_m16(mrow + kl, kvalid, a.mask_vec), kvalid);
+        mask_n = load_m16(mrow + kl, kvalid, a.mask_vec);
+    };
+    const auto fix_bias = [&](int k0, H16 (&b)[T::kQB], uint4 m) {
+        const int kvalid = a.Sk - (k0 + 16 * g);
+        const uint32_t keep = mask_bits16(m, kvalid);
         if (keep != 0xffffu) {
             const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb)
-                fill_bias16(bias_n[qb].lo, bias_n[qb].hi, keep, inside, (half_t)kMaskedLogit,
+                fill_bias16(b[qb].lo, b[qb].hi, keep, inside, (half_t)kMaskedLogit,
                             (half_t)(-INFINITY));
         }
     };
@@ -222,10 +231,12 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         H16 bias16[T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) bias16[qb] = bias_n[qb];
+        const uint4 mask16 = mask_n;
         if (more) {
             fetch(k0 + T::kBK);
             fetch_bm(k0 + T::kBK);
         }
+        fix_bias(k0, bias16, mask16);
 
         // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4
         float4v s[4][T::kQB];
