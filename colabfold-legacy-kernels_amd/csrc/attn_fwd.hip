@@ -34,6 +34,7 @@ struct FwdArgs {
     float scale;
     int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0)
     int mask_vec;  // mask rows are whole 16-byte vectors (Sk % 16 == 0)
+    int head_major;  // work items head-major ([N,H,S,D] tensors), else row-major (packed rows)
 };
 
 template <int DP>
@@ -100,10 +101,12 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
-    // head-major order: an XCD's contiguous run of items covers few heads, so the bias rows
-    // it reads stay in its L2
+    // head-major order for [N,H,S,D] tensors: an XCD's contiguous run of items covers few
+    // heads, so the bias rows it reads stay in its L2; packed rows hold every head of a row n
+    // together, so there the heads of one row run together instead
     const int qt = item % QT, rest = item / QT;
-    const int n = rest % a.N, h = rest / a.N;
+    const int n = a.head_major ? rest % a.N : rest / a.H;
+    const int h = a.head_major ? rest / a.N : rest % a.H;
     const int q0 = qt * T::kBQ;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
@@ -418,6 +421,7 @@ static FwdArgs contiguous_args(int N, int H, int Sq, int Sk, int D) {
     a.Sq = Sq;
     a.Sk = Sk;
     a.D = D;
+    a.head_major = 1;
     return a;
 }
 
