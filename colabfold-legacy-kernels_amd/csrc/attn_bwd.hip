@@ -317,12 +317,14 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 // dK, dV and the dBias partials: S = Q K^T and dP = dO V^T with a lane on one key, so P and dS
 // feed dV^T = dO^T P and dK^T = Q^T dS as B operands straight from registers.
 //
-// A workgroup owns 64 keys (four key groups of 16, one wave each) and QG query groups: for each
-// batch row n of its chunk, query group qg takes query tiles qg, qg + QG, ... of 32 queries,
-// staged by its four waves into its own pair of LDS buffers (one read, one being written, one
-// barrier per tile). Every dBias element (key, q) therefore has one owner wave, which adds its dS
-// in a fixed order; the query groups' dK / dV partials are summed in group order through LDS at
-// the end of each row.
+// A workgroup owns 64 keys (four key groups of 16, one wave each) and QG row groups of its chunk
+// of batch rows: row group rg takes rows n_begin + rg, + QG, ..., and for each row walks all of
+// its query tiles of 32, staged by its four waves into its own pair of LDS buffers (one read, one
+// being written, one barrier per step). A row's dK and dV therefore accumulate in one wave's
+// registers with no cross-wave sum. The row groups walk the tiles of a row from staggered
+// starting tiles, so at every step they add dS into disjoint columns of the fp32 [64 keys][Sq]
+// dBias partial that stays in LDS for the whole chunk: each element is updated by one wave per
+// step, in an order fixed by the schedule.
 //
 // The per-query terms enter the MFMAs as accumulator inputs: S starts from -lse2 / (scale log2e)
 // and dP from -delta (both staged in LDS with the tile), so that s2 = scale log2e S + bias log2e
@@ -339,13 +341,10 @@ struct DkdvTile {
     static constexpr int kLd = DP + 8;
     static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO chunks of one tile
     static constexpr int kCPT = (kChunks + 255) / 256;
-    // halfs per query group and buffer: Q and dO rows, then the tile's -lse2 / c1 and -delta
+    // halfs per row group and buffer: Q and dO rows, then the tile's -lse2 / c1 and -delta
     static constexpr int kRowsHalfs = 2 * kBQ * kLd;
     static constexpr int kStage = kRowsHalfs + 2 * kBQ * 2;
-    static constexpr int kCombineBytes = 4 * (QG - 1) * kDB * kWave * 4 * 4;
-    // two staging buffers per query group; the end-of-row combine of the groups reuses the area
-    static constexpr int kStageBytes =
-        kStage * 2 * 2 * QG > kCombineBytes ? kStage * 2 * 2 * QG : kCombineBytes;
+    static constexpr int kStageBytes = kStage * 2 * 2 * QG;  // two buffers per row group
     // dBias partial [kBK keys][SqA + kDBPad]: the pad staggers the keys' rows across LDS banks
     static constexpr int kDBPad = 4;
 };
@@ -362,20 +361,20 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int n_begin = c * a.chunk;
     const int n_end = min(a.N, n_begin + a.chunk);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int kg = wave & 3, qg = wave >> 2, gtid = tid & 255;
+    const int kg = wave & 3, rg = wave >> 2, gtid = tid & 255;
     const int r16 = lane & 15, g = lane >> 4;
     const int klocal = kg * 16 + r16;
     const int key = kblk * T::kBK + klocal;
     const bool kin = key < a.Sk;
-    const int qtiles = (a.Sq + T::kBQ - 1) / T::kBQ;
-    const int IT = (qtiles + QG - 1) / QG;
-    const int total = (n_end - n_begin) * IT;
+    const int qtiles = (a.Sq + T::kBQ - 1) / T::kBQ;  // at least QG (the host plans QG so)
+    const int stagger = qtiles / QG;                 // tile offset between row groups
+    const int rows = (n_end - n_begin + QG - 1) / QG;  // rows of the busiest row group
+    const int total = rows * qtiles;
 
-    half_t* const stage0 = reinterpret_cast<half_t*>(lds_raw) + qg * T::kStage;
+    half_t* const stage0 = reinterpret_cast<half_t*>(lds_raw) + rg * T::kStage;
     constexpr int kBufStride = QG * T::kStage;  // halfs from buffer 0 to buffer 1 of a group
     const int dbld = a.SqA + T::kDBPad;
     float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][dbld]
-    float* comb = reinterpret_cast<float*>(lds_raw);                   // between rows only
 
     if constexpr (DBIAS) {
         for (int i = tid; i < T::kBK * dbld; i += T::kThreads) DBt[i] = 0.f;
@@ -386,19 +385,27 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const float* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
     constexpr float kDead = kMaskedLogit * kLog2e;  // a dead key's bias times log2e
 
-    // the next tile of this query group: Q / dO chunks and the tile's -lse2 / c1 and -delta
-    // (threads 0..15, one float4 each) to stage, fetched early in a tile; this lane's eight
-    // queries' log2e-scaled bias at its key, fetched once the current ones are consumed (padded
-    // past Sq: -lse2 / c1 infinite, -delta 0, bias 0)
+    // step s of this row group: row n_begin + rg + QG (s / qtiles), query tile
+    // (s % qtiles + rg stagger) % qtiles; a row past n_end is idle
+    const auto row_of = [&](int s) { return n_begin + rg + QG * (s / qtiles); };
+    const auto tile_of = [&](int s) {
+        const int t = s % qtiles + rg * stagger;
+        return t >= qtiles ? t - qtiles : t;
+    };
+
+    // the next step's Q / dO chunks and the tile's -lse2 / c1 and -delta (threads 0..15 of the
+    // group, one float4 each) to stage, fetched early in a step; this lane's eight queries'
+    // log2e-scaled bias at its key, fetched once the current ones are consumed (padded past Sq:
+    // -lse2 / c1 infinite, -delta 0, bias 0)
     struct Pre {
         half8 s[T::kCPT];
         float4v st;
         float4v bt[2];
     };
     Pre pre;
-    const auto fetch_s = [&](Pre& d, int n, int it) {
-        const int qi = it * QG + qg, q0 = qi * T::kBQ;
-        const bool valid = qi < qtiles;
+    const auto fetch_s = [&](Pre& d, int s) {
+        const int n = row_of(s), q0 = tile_of(s) * T::kBQ;
+        const bool valid = n < n_end;
         const int64_t nh = (int64_t)n * a.H + h, base = nh * a.Sq * a.D;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
@@ -414,10 +421,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             d.st = *reinterpret_cast<const float4v*>(src);
         }
     };
-    const auto fetch_c = [&](Pre& d, int it) {
-        const int qi = it * QG + qg, q0 = qi * T::kBQ;
-        if (qi < qtiles) {
-            const float* btp = bt_own + q0;
+    const auto fetch_c = [&](Pre& d, int s) {
+        if (row_of(s) < n_end) {
+            const float* btp = bt_own + tile_of(s) * T::kBQ;
             d.bt[0] = *reinterpret_cast<const float4v*>(btp);
             d.bt[1] = *reinterpret_cast<const float4v*>(btp + 4);
         }
@@ -441,12 +447,13 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         }
     };
 
-    // K and V of the next row as the B operands (lane column = key, slots d = 32 ks + 8 g + j)
-    // and the key's raw mask byte; both operands become zero for a dead key when the row comes
-    // up, so nothing loaded here is examined before then
+    // K and V of this group's next row as the B operands (lane column = key, slots
+    // d = 32 ks + 8 g + j) and the key's raw mask byte; both operands become zero for a dead key
+    // when the row comes up, so nothing loaded here is examined before then
     half8 kopn[T::kKS], vopn[T::kKS];
     uint32_t mbn = 0u;
     const auto fetch_kv = [&](int n) {
+        if (n >= n_end) return;
         const int64_t kbase = ((int64_t)n * a.H + h) * a.Sk * a.D;
         mbn = kin ? (uint32_t)a.kmask[(int64_t)n * a.Sk + key] : 0u;
 #pragma unroll
@@ -463,16 +470,16 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     float4v accv[T::kDB], acck[T::kDB];
 
     if (total > 0) {
-        fetch_kv(n_begin);
-        fetch_s(pre, n_begin, 0);
+        fetch_kv(row_of(0));
+        fetch_s(pre, 0);
         fetch_c(pre, 0);
         stage_tile(pre, 0);
     }
     __syncthreads();
-    for (int t = 0, it = 0, n = n_begin; t < total; ++t) {
+    for (int t = 0; t < total; ++t) {
         const int buf = t & 1;
-        const int qi = it * QG + qg, q0 = qi * T::kBQ;
-        const bool valid = qi < qtiles;
+        const int it = t % qtiles, n = row_of(t), q0 = tile_of(t) * T::kBQ;
+        const bool valid = n < n_end;
         if (it == 0) {
             alive = mbn != 0u;
 #pragma unroll
@@ -486,14 +493,12 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
                 acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
             }
-            if (n + 1 < n_end) fetch_kv(n + 1);
+            fetch_kv(n + QG);
         }
         const half_t* Qs = stage0 + buf * kBufStride;
         const half_t* Os = Qs + T::kBQ * T::kLd;
         const float* Ls = reinterpret_cast<const float*>(Qs + T::kRowsHalfs);  // -lse2 / c1, -delta
-        const bool wrap = it + 1 == IT;
-        const int n_next = wrap ? n + 1 : n, it_next = wrap ? 0 : it + 1;
-        if (t + 1 < total) fetch_s(pre, n_next, it_next);
+        if (t + 1 < total) fetch_s(pre, t + 1);
 
         // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
         // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
@@ -518,6 +523,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1, bt[i]);
             }
         }
+
         half8 pb, dsb;
         if (valid) {
             float dsf[8];
@@ -535,8 +541,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) dsb[j] = (half_t)dsf[j];
             if constexpr (DBIAS) {
-                // this lane is the only writer of these eight elements, so the order is fixed
-                // (a read-modify-write: LDS float atomics measured several times slower here)
+                // the row groups' tiles are disjoint at every step, and this lane is the only
+                // writer of these eight elements within its group (a read-modify-write: LDS float
+                // atomics measured several times slower here)
                 float* row = DBt + klocal * dbld + q0 + 8 * g;
                 float4 lo = *reinterpret_cast<float4*>(row);
                 float4 hi = *reinterpret_cast<float4*>(row + 4);
@@ -546,11 +553,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 *reinterpret_cast<float4*>(row + 4) = hi;
             }
         }
-        // the next tile's accumulator inputs and bias, into the registers just consumed
-        if (t + 1 < total) fetch_c(pre, it_next);
+        // the next step's bias, into the registers just consumed
+        if (t + 1 < total) fetch_c(pre, t + 1);
 
         if (valid) {
-
             // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
             // its k-slots queries 8 g + j, read transposed from the row-major tiles
             const auto orow = [&](int r) { return Os + perm_row(r, 8) * T::kLd; };
@@ -562,46 +568,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 accv[db] = mfma16x16x32(ot, pb, accv[db]);
                 acck[db] = mfma16x16x32(qt, dsb, acck[db]);
             }
-        }
-
-        if (it == IT - 1) {
-            if constexpr (QG > 1) {
-                // the query groups' partials, summed in group order by group 0 (two rounds); the
-                // staging area is free: every wave is past this tile's reads, and the next tile
-                // is staged below
-                float* slot = comb + ((kg * (QG - 1) + qg - 1) * T::kDB) * 256 + lane * 4;
-                __syncthreads();
-                if (qg > 0) {
-#pragma unroll
-                    for (int db = 0; db < T::kDB; ++db) *reinterpret_cast<float4v*>(slot + db * 256) = acck[db];
-                }
-                __syncthreads();
-                if (qg == 0) {
-#pragma unroll
-                    for (int o = 0; o < QG - 1; ++o)
-#pragma unroll
-                        for (int db = 0; db < T::kDB; ++db)
-                            acck[db] += *reinterpret_cast<const float4v*>(
-                                comb + ((kg * (QG - 1) + o) * T::kDB + db) * 256 + lane * 4);
-                }
-                __syncthreads();
-                if (qg > 0) {
-#pragma unroll
-                    for (int db = 0; db < T::kDB; ++db) *reinterpret_cast<float4v*>(slot + db * 256) = accv[db];
-                }
-                __syncthreads();
-                if (qg == 0) {
-#pragma unroll
-                    for (int o = 0; o < QG - 1; ++o)
-#pragma unroll
-                        for (int db = 0; db < T::kDB; ++db)
-                            accv[db] += *reinterpret_cast<const float4v*>(
-                                comb + ((kg * (QG - 1) + o) * T::kDB + db) * 256 + lane * 4);
-                }
-                __syncthreads();
-            }
-            if (qg == 0 && kin) {
-                // lane holds d = (DP/4) g .. +DP/4 of its key
+            if (it == qtiles - 1 && kin) {
+                // the row is done: lane holds d = (DP/4) g .. +DP/4 of its key
                 const int64_t off = ((int64_t)n * a.H + h) * a.Sk * a.D + (int64_t)key * a.D;
 #pragma unroll
                 for (int cc = 0; cc < DP / 32; ++cc) {
@@ -618,13 +586,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 }
             }
         }
-        // the other buffer was last read a tile ago, before the barrier that ended that tile
+        // the other buffer was last read a step ago, before the barrier that ended that step
         if (t + 1 < total) stage_tile(pre, buf ^ 1);
         __syncthreads();
-        if (++it == IT) {
-            it = 0;
-            ++n;
-        }
     }
 
     if constexpr (DBIAS) {
@@ -768,7 +732,11 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.SkA = p.kblocks * 64;
     p.dbias_lds = (size_t)64 * (p.SqA + 4) * sizeof(float);  // the dK/dV kernel's [64][SqA + 4]
     const int limit = shared_limit(device);
-    const int qg_max = p.DP == 32 ? 4 : 2;
+    // row groups of the dK/dV kernel: at most the query tiles of a row, which they walk from
+    // staggered starts
+    const int64_t qtiles = std::max<int64_t>((Sq + 31) / 32, 1);
+    int qg_max = p.DP == 32 ? 4 : 2;
+    while (qg_max > qtiles) qg_max /= 2;
     p.QG = 0;
     for (int qg = qg_max; qg >= 1; qg /= 2) {
         const size_t need = dkdv_stage_bytes(p.DP, qg) + p.dbias_lds;
@@ -793,11 +761,14 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
     int64_t best = 1, best_cost = INT64_MAX;
     for (int64_t ch = 1; ch <= Nr; ++ch) {
-        const int64_t rows = (Nr + ch - 1) / ch;
+        // rows per workgroup, a whole number of passes of its QG row groups where N allows
+        const int64_t rows = std::min<int64_t>(((Nr + ch - 1) / ch + p.QG - 1) / p.QG * p.QG, Nr);
         const int64_t real = (Nr + rows - 1) / rows;
         const int64_t rounds = (real * cols + slots - 1) / slots;
-        // each extra chunk adds a dbias partial to write and sum; a row costs about 24 of them
-        const int64_t cost = rounds * rows * 24 + real;
+        const int64_t passes = (rows + p.QG - 1) / p.QG;
+        // each extra chunk adds a dbias partial to write and sum; a pass of the row groups costs
+        // about 24 of them per row group
+        const int64_t cost = rounds * passes * p.QG * 24 + real;
         if (cost < best_cost) {
             best_cost = cost;
             best = real;
