@@ -394,9 +394,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     };
 
     // the next step's Q / dO chunks and the tile's -lse2 / c1 and -delta (threads 0..15 of the
-    // group, one float4 each) to stage, fetched early in a step; this lane's eight queries'
-    // log2e-scaled bias at its key, fetched once the current ones are consumed (padded past Sq:
-    // -lse2 / c1 infinite, -delta 0, bias 0)
+    // group, one float4 each) to stage, fetched right after the previous stage; this lane's
+    // eight queries' log2e-scaled bias at its key, fetched once the current ones are consumed
+    // (padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0)
     struct Pre {
         half8 s[T::kCPT];
         float4v st;
@@ -474,6 +474,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         fetch_s(pre, 0);
         fetch_c(pre, 0);
         stage_tile(pre, 0);
+        if (total > 1) fetch_s(pre, 1);
     }
     __syncthreads();
     for (int t = 0; t < total; ++t) {
@@ -498,7 +499,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const half_t* Qs = stage0 + buf * kBufStride;
         const half_t* Os = Qs + T::kBQ * T::kLd;
         const float* Ls = reinterpret_cast<const float*>(Qs + T::kRowsHalfs);  // -lse2 / c1, -delta
-        if (t + 1 < total) fetch_s(pre, t + 1);
 
         // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
         // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
@@ -586,8 +586,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 }
             }
         }
-        // the other buffer was last read a step ago, before the barrier that ended that step
+        // the other buffer was last read a step ago, before the barrier that ended that step;
+        // the chunks for the step after next are fetched at once, a whole step ahead of their
+        // stage
         if (t + 1 < total) stage_tile(pre, buf ^ 1);
+        if (t + 2 < total) fetch_s(pre, t + 2);
         __syncthreads();
     }
 
