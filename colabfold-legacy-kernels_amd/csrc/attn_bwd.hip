@@ -393,17 +393,20 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         return t >= qtiles ? t - qtiles : t;
     };
 
-    // the next step's Q / dO chunks and the tile's -lse2 / c1 and -delta (threads 0..15 of the
-    // group, one float4 each) to stage, fetched right after the previous stage; this lane's
-    // eight queries' log2e-scaled bias at its key, fetched once the current ones are consumed
-    // (padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0)
-    struct Pre {
+    // A step's Q / dO chunks and the tile's -lse2 / c1 and -delta (threads 0..15 of the group,
+    // one float4 each) to stage; two register sets, one per step parity, fetched two steps ahead
+    // of their stage. This lane's eight queries' log2e-scaled bias at its key, fetched once the
+    // current ones are consumed. (Padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0.)
+    struct Chunks {
         half8 s[T::kCPT];
         float4v st;
+    };
+    struct Pre {
         float4v bt[2];
     };
+    Chunks ch0, ch1;
     Pre pre;
-    const auto fetch_s = [&](Pre& d, int s) {
+    const auto fetch_s = [&](Chunks& d, int s) {
         const int n = row_of(s), q0 = tile_of(s) * T::kBQ;
         const bool valid = n < n_end;
         const int64_t nh = (int64_t)n * a.H + h, base = nh * a.Sq * a.D;
@@ -428,7 +431,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             d.bt[1] = *reinterpret_cast<const float4v*>(btp + 4);
         }
     };
-    const auto stage_tile = [&](const Pre& d, int buf) {
+    const auto stage_tile = [&](const Chunks& d, int buf) {
         half_t* Qs = stage0 + buf * kBufStride;
         half_t* Os = Qs + T::kBQ * T::kLd;
 #pragma unroll
@@ -471,13 +474,16 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     if (total > 0) {
         fetch_kv(row_of(0));
-        fetch_s(pre, 0);
+        fetch_s(ch0, 0);
+        if (total > 1) fetch_s(ch1, 1);
         fetch_c(pre, 0);
-        stage_tile(pre, 0);
-        if (total > 1) fetch_s(pre, 1);
+        stage_tile(ch0, 0);
+        if (total > 2) fetch_s(ch0, 2);
     }
     __syncthreads();
-    for (int t = 0; t < total; ++t) {
+    // step t reads LDS buffer t & 1; at its end it stages step t + 1 from the register set of
+    // that parity and refills the set with step t + 3
+    const auto step = [&](int t, Chunks& next) {
         const int buf = t & 1;
         const int it = t % qtiles, n = row_of(t), q0 = tile_of(t) * T::kBQ;
         const bool valid = n < n_end;
@@ -586,12 +592,14 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 }
             }
         }
-        // the other buffer was last read a step ago, before the barrier that ended that step;
-        // the chunks for the step after next are fetched at once, a whole step ahead of their
-        // stage
-        if (t + 1 < total) stage_tile(pre, buf ^ 1);
-        if (t + 2 < total) fetch_s(pre, t + 2);
+        // the other buffer was last read a step ago, before the barrier that ended that step
+        if (t + 1 < total) stage_tile(next, buf ^ 1);
+        if (t + 3 < total) fetch_s(next, t + 3);
         __syncthreads();
+    };
+    for (int t = 0; t < total; t += 2) {
+        step(t, ch1);
+        if (t + 1 < total) step(t + 1, ch0);
     }
 
     if constexpr (DBIAS) {
