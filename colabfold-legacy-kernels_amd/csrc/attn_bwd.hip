@@ -10,8 +10,8 @@
 //
 // Where the reference adds dQ and dBias with fp32 atomics into global memory, this backward is
 // three kernels with no atomics, so every result is bit-identical from run to run:
-//   biast_kernel  bias * log2e as fp32, transposed to [H][keys][queries] and zero-padded, so a
-//                 dK/dV lane reads its eight queries' bias at its key with two vector loads.
+//   biast_kernel  bias transposed to [H][keys][queries] (fp16, zero-padded), so a dK/dV lane
+//                 reads its eight queries' bias at its key with one 16-byte load.
 //   dq_kernel     one workgroup per (n, h, 128 queries), looping over key tiles as the forward
 //                 does: dQ^T = K^T dS^T accumulates in registers; it also writes delta and lse2
 //                 padded to whole 32-query tiles (0 and +inf past Sq).
@@ -40,7 +40,7 @@ struct BwdArgs {
     float* dbias;
     float* delta;    // workspace [N, H, SqA]: -rowsum(out * dout), 0 past Sq
     float* lse2p;    // workspace [N, H, SqA]: -lse / c1, -inf past Sq
-    float* biast;    // workspace [H, SkA, SqA]: bias[h][q][key] * log2e, 0 outside
+    half_t* biast;   // workspace [H, SkA, SqA]: bias[h][q][key], 0 outside
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
     int N, H, Sq, Sk, D;
     int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
@@ -49,6 +49,7 @@ struct BwdArgs {
     int chunks;
     float scale;
     float c1;    // scale log2e, or 1 where |scale log2e| is below 1e-30
+    float c1s;   // c1 / log2e: scale, or the stand-in's 1 / log2e
     int kscale;  // 0 where c1 stands in for a negligible scale: the dK/dV kernel's K is then zero
     int bias_vec, mask_vec;
 };
@@ -381,9 +382,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 
     const float scale = a.scale;
-    const float c1 = a.c1;  // scale log2e, or 1 where that is below fp32 resolution (K is zero then)
-    const float* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
-    constexpr float kDead = kMaskedLogit * kLog2e;  // a dead key's bias times log2e
+    const float c1s = a.c1s;  // scale, or the stand-in for a negligible scale (K is zero then)
+    const half_t* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
 
     // step s of this row group: row n_begin + rg + QG (s / qtiles), query tile
     // (s % qtiles + rg stagger) % qtiles; a row past n_end is idle
@@ -394,18 +394,15 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     };
 
     // A step's Q / dO chunks and the tile's -lse2 / c1 and -delta (threads 0..15 of the group,
-    // one float4 each) to stage; two register sets, one per step parity, fetched two steps ahead
-    // of their stage. This lane's eight queries' log2e-scaled bias at its key, fetched once the
-    // current ones are consumed. (Padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0.)
+    // one float4 each) to stage, and this lane's eight queries' bias at its key: two register
+    // sets of each, one per step parity, fetched two steps ahead of their use. (Padded past Sq:
+    // -lse2 / c1 infinite, -delta 0, bias 0.)
     struct Chunks {
         half8 s[T::kCPT];
         float4v st;
     };
-    struct Pre {
-        float4v bt[2];
-    };
     Chunks ch0, ch1;
-    Pre pre;
+    half8 bt0, bt1;
     const auto fetch_s = [&](Chunks& d, int s) {
         const int n = row_of(s), q0 = tile_of(s) * T::kBQ;
         const bool valid = n < n_end;
@@ -424,12 +421,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             d.st = *reinterpret_cast<const float4v*>(src);
         }
     };
-    const auto fetch_c = [&](Pre& d, int s) {
-        if (row_of(s) < n_end) {
-            const float* btp = bt_own + tile_of(s) * T::kBQ;
-            d.bt[0] = *reinterpret_cast<const float4v*>(btp);
-            d.bt[1] = *reinterpret_cast<const float4v*>(btp + 4);
-        }
+    const auto fetch_c = [&](half8& d, int s) {
+        if (row_of(s) < n_end) d = bld8(bt_own + tile_of(s) * T::kBQ);
     };
     const auto stage_tile = [&](const Chunks& d, int buf) {
         half_t* Qs = stage0 + buf * kBufStride;
@@ -476,14 +469,16 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         fetch_kv(row_of(0));
         fetch_s(ch0, 0);
         if (total > 1) fetch_s(ch1, 1);
-        fetch_c(pre, 0);
+        fetch_c(bt0, 0);
+        if (total > 1) fetch_c(bt1, 1);
         stage_tile(ch0, 0);
         if (total > 2) fetch_s(ch0, 2);
     }
     __syncthreads();
-    // step t reads LDS buffer t & 1; at its end it stages step t + 1 from the register set of
-    // that parity and refills the set with step t + 3
-    const auto step = [&](int t, Chunks& next) {
+    // step t reads LDS buffer t & 1 and the bias set of its parity, which it refills with step
+    // t + 2 once consumed; at its end it stages step t + 1 from the chunk set of that parity and
+    // refills the set with step t + 3
+    const auto step = [&](int t, Chunks& next, half8& bt) {
         const int buf = t & 1;
         const int it = t % qtiles, n = row_of(t), q0 = tile_of(t) * T::kBQ;
         const bool valid = n < n_end;
@@ -523,10 +518,12 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                     s = mfma16x16x32(qa, kop[ks], s);
                     dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
                 }
-                // a dead key's bias is the masked logit
-                const float4v bt = all_alive || alive ? pre.bt[qb] : float4v{kDead, kDead, kDead, kDead};
+                // s2 = log2e (scale S + bias), a dead key's bias being the masked logit
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1, bt[i]);
+                for (int i = 0; i < 4; ++i) {
+                    const half_t b = all_alive || alive ? bt[4 * qb + i] : (half_t)kMaskedLogit;
+                    x[4 * qb + i] = fmaf(s[i], c1s, (float)b) * kLog2e;
+                }
             }
         }
 
@@ -559,8 +556,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 *reinterpret_cast<float4*>(row + 4) = hi;
             }
         }
-        // the next step's bias, into the registers just consumed
-        if (t + 1 < total) fetch_c(pre, t + 1);
+        // the bias two steps on, into the registers just consumed
+        if (t + 2 < total) fetch_c(bt, t + 2);
 
         if (valid) {
             // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
@@ -598,8 +595,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         __syncthreads();
     };
     for (int t = 0; t < total; t += 2) {
-        step(t, ch1);
-        if (t + 1 < total) step(t + 1, ch0);
+        step(t, ch1, bt0);
+        if (t + 1 < total) step(t + 1, ch0, bt1);
     }
 
     if constexpr (DBIAS) {
@@ -610,11 +607,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
-// biast[h][key][q] = bias[h][q][key] * log2e for q < Sq, key < Sk, else 0, over [H][SkA][SqA]:
-// a workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads where the bias
-// rows allow them and 16-byte stores (SqA is a multiple of 32).
+// biast[h][key][q] = bias[h][q][key] for q < Sq, key < Sk, else 0, over [H][SkA][SqA]: a
+// workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads where the bias rows
+// allow them and 16-byte stores (SqA is a multiple of 32).
 __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
-    __shared__ float tile[32][65];
+    __shared__ half_t tile[32][66];
     const int qtiles = a.SqA / 32;
     const int item = blockIdx.x;
     const int qt = item % qtiles, rest = item / qtiles;
@@ -634,16 +631,15 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
             for (int j = 0; j < 8; ++j) b[j] = j < valid ? src[j] : (half_t)0.f;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) tile[qq][kc + j] = (float)b[j] * kLog2e;
+        for (int j = 0; j < 8; ++j) tile[qq][kc + j] = b[j];
     }
     __syncthreads();
     {
         const int kk = tid / 4, qc = (tid % 4) * 8;
-        float* dst = a.biast + ((int64_t)h * a.SkA + k0 + kk) * a.SqA + q0 + qc;
-        *reinterpret_cast<float4*>(dst) =
-            make_float4(tile[qc][kk], tile[qc + 1][kk], tile[qc + 2][kk], tile[qc + 3][kk]);
-        *reinterpret_cast<float4*>(dst + 4) =
-            make_float4(tile[qc + 4][kk], tile[qc + 5][kk], tile[qc + 6][kk], tile[qc + 7][kk]);
+        half8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = tile[qc + j][kk];
+        *reinterpret_cast<half8*>(a.biast + ((int64_t)h * a.SkA + k0 + kk) * a.SqA + q0 + qc) = o;
     }
 }
 
@@ -788,7 +784,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
     p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // delta, and lse2 after it
-    p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(float));
+    p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(half_t));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     return p;
 }
@@ -917,7 +913,7 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     char* ws = static_cast<char*>(workspace);
     a.delta = reinterpret_cast<float*>(ws);
     a.lse2p = reinterpret_cast<float*>(ws + p.delta_bytes);
-    a.biast = reinterpret_cast<float*>(ws + 2 * p.delta_bytes);
+    a.biast = reinterpret_cast<half_t*>(ws + 2 * p.delta_bytes);
     a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
     a.SqA = p.SqA;
@@ -929,6 +925,7 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.c1 = scale * kLog2e;
     a.kscale = fabsf(a.c1) >= 1e-30f;
     if (!a.kscale) a.c1 = 1.f;  // scale log2e S is below fp32 resolution against the bias
+    a.c1s = a.c1 / kLog2e;
     a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
     a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);

@@ -121,11 +121,12 @@ def test_stage_hook_bounds(lib):
 @pytest.mark.parametrize("n,h,sq,sk,d", [(0, 2, 24, 40, 32), (2, 2, 0, 40, 32), (2, 2, 24, 0, 32),
                                          (512, 8, 384, 384, 32), (3, 4, 70, 83, 16), (1, 1, 1, 1, 96)])
 def test_backward_workspace_size(lib, n, h, sq, sk, d):
-    """The workspace holds delta and lse2 (padded to 32 queries), the transposed bias (keys padded
-    to 64) and the dBias partials: never less than those arrays, also for empty problems."""
+    """The workspace holds delta and lse2 (fp32, padded to 32 queries), the fp16 transposed bias
+    (keys padded to 64) and the dBias partials: never less than those arrays, also for empty
+    problems."""
     q, _ = buf(F16, n, h, sq, d)
     k, _ = buf(F16, n, h, sk, d)
     size = lib.clk_attention_bwd_workspace_size(0, q, k)
     sqa, ska = -(-sq // 32) * 32, -(-sk // 64) * 64
-    assert size >= 4 * (2 * n * h * sqa + h * ska * sqa)
+    assert size >= 4 * 2 * n * h * sqa + 2 * h * ska * sqa
     assert size % 256 == 0
