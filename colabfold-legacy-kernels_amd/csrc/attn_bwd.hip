@@ -368,9 +368,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int key = kblk * T::kBK + klocal;
     const bool kin = key < a.Sk;
     const int qtiles = (a.Sq + T::kBQ - 1) / T::kBQ;  // at least QG (the host plans QG so)
+    const int qsteps = (qtiles + 1) & ~1;            // steps per row: even, an odd count padded
     const int stagger = qtiles / QG;                 // tile offset between row groups
-    const int rows = (n_end - n_begin + QG - 1) / QG;  // rows of the busiest row group
-    const int total = rows * qtiles;
+    const int rows = (n_end - n_begin + QG - 1) / QG;  // row passes of the busiest row group
+    const int total = rows * qsteps;
 
     half_t* const stage0 = reinterpret_cast<half_t*>(lds_raw) + rg * T::kStage;
     constexpr int kBufStride = QG * T::kStage;  // halfs from buffer 0 to buffer 1 of a group
@@ -385,57 +386,60 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const float c1s = a.c1s;  // scale, or the stand-in for a negligible scale (K is zero then)
     const half_t* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
 
-    // step s of this row group: row n_begin + rg + QG (s / qtiles), query tile
-    // (s % qtiles + rg stagger) % qtiles; a row past n_end is idle
-    const auto row_of = [&](int s) { return n_begin + rg + QG * (s / qtiles); };
-    const auto tile_of = [&](int s) {
-        const int t = s % qtiles + rg * stagger;
-        return t >= qtiles ? t - qtiles : t;
+    // Step t of this row group is query tile tile_of(t % qsteps) of row row_of(t); a step past
+    // the row's tiles, or of a row past n_end, is idle. Every load below is issued
+    // unconditionally from a valid (clamped) address and judged only where it is used, so the
+    // loop body is straight-line and each wait covers exactly the loads it needs.
+    const auto row_of = [&](int t) { return n_begin + rg + QG * (t / qsteps); };
+    const auto tile_of = [&](int it) {
+        const int x = (it < qtiles ? it : 0) + rg * stagger;
+        return x >= qtiles ? x - qtiles : x;
     };
 
-    // A step's Q / dO chunks and the tile's -lse2 / c1 and -delta (threads 0..15 of the group,
-    // one float4 each) to stage, and this lane's eight queries' bias at its key: two register
-    // sets of each, one per step parity, fetched two steps ahead of their use. (Padded past Sq:
-    // -lse2 / c1 infinite, -delta 0, bias 0.)
+    // A step's Q / dO chunks with their in-range bits, and the tile's -lse2 / c1 and -delta (one
+    // float4 per lane; lanes 0..15 of the group stage them): two register sets, one per step
+    // parity, fetched two steps ahead of their stage. This lane's eight queries' bias at its key:
+    // two register sets likewise, two steps ahead of their use. (Padded past Sq: -lse2 / c1
+    // infinite, -delta 0, bias 0.)
     struct Chunks {
         half8 s[T::kCPT];
+        uint32_t ok;
         float4v st;
     };
     Chunks ch0, ch1;
     half8 bt0, bt1;
-    const auto fetch_s = [&](Chunks& d, int s) {
-        const int n = row_of(s), q0 = tile_of(s) * T::kBQ;
-        const bool valid = n < n_end;
-        const int64_t nh = (int64_t)n * a.H + h, base = nh * a.Sq * a.D;
+    const auto fetch_s = [&](Chunks& d, int t) {
+        const int n = row_of(t), it = t % qsteps, q0 = tile_of(it) * T::kBQ;
+        const bool nv = n < n_end && it < qtiles;
+        const int64_t nh = (int64_t)(nv ? n : n_begin) * a.H + h, base = nh * a.Sq * a.D;
+        d.ok = 0u;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int cc = gtid + i * 256;
+            const int cc = gtid + i * 256;  // every (Q, dO) x row x column chunk: kChunks = 256 kCPT
             const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
             const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
-            const bool ok = valid && cc < T::kChunks && q0 + row < a.Sq && col < a.D;
+            const bool ok = nv && q0 + row < a.Sq && col < a.D;
             const half_t* src = which ? a.dout : a.q;
-            d.s[i] = ok ? bld8(src + base + (int64_t)(q0 + row) * a.D + col) : bzero8();
+            const int qr = q0 + row < a.Sq ? q0 + row : a.Sq - 1;
+            d.s[i] = bld8(src + base + (int64_t)qr * a.D + (col < a.D ? col : 0));
+            d.ok |= (uint32_t)ok << i;
         }
-        if (valid && gtid < 16) {
-            const float* src = (gtid < 8 ? a.lse2p : a.delta) + nh * a.SqA + q0 + 4 * (gtid & 7);
-            d.st = *reinterpret_cast<const float4v*>(src);
-        }
+        const int l16 = gtid & 15;
+        const float* src = (l16 < 8 ? a.lse2p : a.delta) + nh * a.SqA + q0 + 4 * (l16 & 7);
+        d.st = *reinterpret_cast<const float4v*>(src);
     };
-    const auto fetch_c = [&](half8& d, int s) {
-        if (row_of(s) < n_end) d = bld8(bt_own + tile_of(s) * T::kBQ);
-    };
+    const auto fetch_c = [&](half8& d, int t) { d = bld8(bt_own + tile_of(t % qsteps) * T::kBQ); };
     const auto stage_tile = [&](const Chunks& d, int buf) {
         half_t* Qs = stage0 + buf * kBufStride;
         half_t* Os = Qs + T::kBQ * T::kLd;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
             const int cc = gtid + i * 256;
-            if (cc < T::kChunks) {
-                const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
-                const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
-                half_t* rm = which ? Os : Qs;
-                *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) = d.s[i];
-            }
+            const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
+            const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
+            half_t* rm = which ? Os : Qs;
+            *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) =
+                (d.ok >> i) & 1u ? d.s[i] : bzero8();
         }
         if (gtid < 16) {
             // [-lse2 / c1 of the 32 queries][-delta of the 32 queries]
@@ -445,58 +449,44 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 
     // K and V of this group's next row as the B operands (lane column = key, slots
     // d = 32 ks + 8 g + j) and the key's raw mask byte; both operands become zero for a dead key
-    // when the row comes up, so nothing loaded here is examined before then
+    // when the row comes up
     half8 kopn[T::kKS], vopn[T::kKS];
     uint32_t mbn = 0u;
-    const auto fetch_kv = [&](int n) {
-        if (n >= n_end) return;
-        const int64_t kbase = ((int64_t)n * a.H + h) * a.Sk * a.D;
-        mbn = kin ? (uint32_t)a.kmask[(int64_t)n * a.Sk + key] : 0u;
+    const auto fetch_kv = [&](int pass) {
+        const int n = n_begin + rg + QG * pass;
+        const int64_t nh = (int64_t)(n < n_end ? n : n_begin) * a.H + h;
+        const int kc = kin ? key : 0;
+        mbn = (uint32_t)a.kmask[(nh / a.H) * a.Sk + kc];
 #pragma unroll
         for (int ks = 0; ks < T::kKS; ++ks) {
             const int d0 = 32 * ks + 8 * g;
-            const bool ok = kin && d0 < a.D;
-            kopn[ks] = ok && a.kscale ? bld8(a.k + kbase + (int64_t)key * a.D + d0) : bzero8();
-            vopn[ks] = ok ? bld8(a.v + kbase + (int64_t)key * a.D + d0) : bzero8();
+            const int64_t off = nh * a.Sk * a.D + (int64_t)kc * a.D + (d0 < a.D ? d0 : 0);
+            kopn[ks] = bld8(a.k + off);
+            vopn[ks] = bld8(a.v + off);
         }
     };
 
     half8 kop[T::kKS], vop[T::kKS];
-    bool alive = false, all_alive = true;
+    bool alive = false, all_alive = true, nv = false;
     float4v accv[T::kDB], acck[T::kDB];
 
     if (total > 0) {
-        fetch_kv(row_of(0));
+        fetch_kv(0);
         fetch_s(ch0, 0);
-        if (total > 1) fetch_s(ch1, 1);
+        fetch_s(ch1, min(1, total - 1));
         fetch_c(bt0, 0);
-        if (total > 1) fetch_c(bt1, 1);
+        fetch_c(bt1, min(1, total - 1));
         stage_tile(ch0, 0);
-        if (total > 2) fetch_s(ch0, 2);
+        fetch_s(ch0, min(2, total - 1));
     }
     __syncthreads();
+
     // step t reads LDS buffer t & 1 and the bias set of its parity, which it refills with step
     // t + 2 once consumed; at its end it stages step t + 1 from the chunk set of that parity and
-    // refills the set with step t + 3
+    // refills the set with step t + 3 (steps past the end load the last step again, unused)
     const auto step = [&](int t, Chunks& next, half8& bt) {
-        const int buf = t & 1;
-        const int it = t % qtiles, n = row_of(t), q0 = tile_of(t) * T::kBQ;
-        const bool valid = n < n_end;
-        if (it == 0) {
-            alive = mbn != 0u;
-#pragma unroll
-            for (int ks = 0; ks < T::kKS; ++ks) {
-                kop[ks] = alive ? kopn[ks] : bzero8();
-                vop[ks] = alive ? vopn[ks] : bzero8();
-            }
-            all_alive = __all(alive);
-#pragma unroll
-            for (int db = 0; db < T::kDB; ++db) {
-                accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
-                acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
-            }
-            fetch_kv(n + QG);
-        }
+        const int buf = t & 1, it = t % qsteps, q0 = tile_of(it) * T::kBQ;
+        const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
         const half_t* Os = Qs + T::kBQ * T::kLd;
         const float* Ls = reinterpret_cast<const float*>(Qs + T::kRowsHalfs);  // -lse2 / c1, -delta
@@ -526,9 +516,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 }
             }
         }
+        fetch_c(bt, min(t + 2, total - 1));  // the bias two steps on, into the registers just consumed
 
-        half8 pb, dsb;
         if (valid) {
+            half8 pb, dsb;
             float dsf[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -555,11 +546,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 *reinterpret_cast<float4*>(row) = lo;
                 *reinterpret_cast<float4*>(row + 4) = hi;
             }
-        }
-        // the bias two steps on, into the registers just consumed
-        if (t + 2 < total) fetch_c(bt, t + 2);
 
-        if (valid) {
             // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
             // its k-slots queries 8 g + j, read transposed from the row-major tiles
             const auto orow = [&](int r) { return Os + perm_row(r, 8) * T::kLd; };
@@ -571,32 +558,52 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 accv[db] = mfma16x16x32(ot, pb, accv[db]);
                 acck[db] = mfma16x16x32(qt, dsb, acck[db]);
             }
-            if (it == qtiles - 1 && kin) {
-                // the row is done: lane holds d = (DP/4) g .. +DP/4 of its key
-                const int64_t off = ((int64_t)n * a.H + h) * a.Sk * a.D + (int64_t)key * a.D;
-#pragma unroll
-                for (int cc = 0; cc < DP / 32; ++cc) {
-                    const int d0 = (DP / 4) * g + 8 * cc;
-                    if (d0 >= a.D) continue;
-                    half8 ok, ov;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
-                        ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
-                    }
-                    *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
-                    *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
-                }
-            }
         }
         // the other buffer was last read a step ago, before the barrier that ended that step
-        if (t + 1 < total) stage_tile(next, buf ^ 1);
-        if (t + 3 < total) fetch_s(next, t + 3);
+        stage_tile(next, buf ^ 1);
+        fetch_s(next, min(t + 3, total - 1));
         __syncthreads();
     };
-    for (int t = 0; t < total; t += 2) {
-        step(t, ch1, bt0);
-        if (t + 1 < total) step(t + 1, ch0, bt1);
+
+    for (int pass = 0; pass < rows; ++pass) {
+        const int n = n_begin + rg + QG * pass;
+        nv = n < n_end;
+        alive = nv && kin && mbn != 0u;
+#pragma unroll
+        for (int ks = 0; ks < T::kKS; ++ks) {
+            kop[ks] = alive && a.kscale && 32 * ks + 8 * g < a.D ? kopn[ks] : bzero8();
+            vop[ks] = alive && 32 * ks + 8 * g < a.D ? vopn[ks] : bzero8();
+        }
+        all_alive = __all(alive);
+#pragma unroll
+        for (int db = 0; db < T::kDB; ++db) {
+            accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
+            acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
+        }
+        fetch_kv(pass + 1 < rows ? pass + 1 : pass);
+
+        for (int it = 0; it < qsteps; it += 2) {
+            step(pass * qsteps + it, ch1, bt0);
+            step(pass * qsteps + it + 1, ch0, bt1);
+        }
+
+        if (nv && kin) {
+            // the row is done: lane holds d = (DP/4) g .. +DP/4 of its key
+            const int64_t off = ((int64_t)n * a.H + h) * a.Sk * a.D + (int64_t)key * a.D;
+#pragma unroll
+            for (int cc = 0; cc < DP / 32; ++cc) {
+                const int d0 = (DP / 4) * g + 8 * cc;
+                if (d0 >= a.D) continue;
+                half8 ok, ov;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
+                    ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
+                }
+                *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
+                *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
+            }
+        }
     }
 
     if constexpr (DBIAS) {
