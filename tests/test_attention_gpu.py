@@ -85,7 +85,7 @@ def check(got, ref, label, absolute=True):
 
 @pytest.mark.parametrize("kw", [dict(sq=96, sk=96, d=32), dict(sq=96, sk=96, d=32, bq=64, bk=64),
                                 dict(sq=64, sk=64, d=64, bk=64), dict(sq=70, sk=83, d=16),
-                                dict(sq=128, sk=32, d=8, n=1, h=1)])
+                                dict(sq=128, sk=32, d=8, n=1, h=1), dict(sq=200, sk=208, d=32, n=2)])
 def test_base_shapes(hip, kw):
     got, ref = run(hip, **kw)
     check(got, ref, str(kw))
