@@ -16,6 +16,8 @@
 // product out^T = W X^T, whose accumulator gives a lane 8 consecutive columns of one row (a
 // 16-byte store); channel-major results use out = X W^T, giving a lane 16 consecutive rows of
 // one channel.
+#include <type_traits>
+
 #include "clk_common.h"
 
 namespace clk {
@@ -331,6 +333,159 @@ __global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
             }
         }
     }
+}
+
+// The same projection with a fixed shape of work, for the common case: no keep mask, and every
+// wave owning exactly PAIRS column pairs (all four row blocks). Each wave then issues a fixed
+// number of stores per tile, and the next tile's rows are prefetched unconditionally (clamped to
+// the last tile), so the loop over whole tiles is straight-line: the wait for the prefetched rows
+// covers only them, not the stores issued after them. The partial last tile, if any, follows the
+// loop with per-row checks.
+// At K = 64 two workgroups share a CU (LDS allows it), so the kernel is held to 128 VGPRs.
+template <int K, bool LN, int TH, int PAIRS>
+__global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs a) {
+    constexpr int KS = K / 32, TW = TH / kWave, NP = PAIRS * TW;
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    const int col0 = blockIdx.y * a.cols;
+    const bool do_heads = blockIdx.y == 0 && a.heads > 0;
+    half_t* Wf = lds;                           // NP * 2 blocks
+    half_t* Hf = Wf + NP * 32 * K;              // one block of head rows
+    half_t* Xf = Hf + (do_heads ? 16 * K : 0);  // 4 row blocks
+    float* sc = reinterpret_cast<float*>(Xf + kTileRows * K);
+    float* of = sc + K;
+
+    load_weight_frags<K, true>(Wf, a.wT, NP * 32, 2 * NP, col0);
+    if (do_heads) load_weight_frags<K, false>(Hf, a.wbT, a.heads, 1);
+    if constexpr (LN) {
+        for (int i = threadIdx.x; i < K; i += TH) {
+            sc[i] = a.scale[i];
+            of[i] = a.offset[i];
+        }
+    }
+
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows, full = a.M / kTileRows;
+    const bool heads_wave = do_heads && wave == TW - 1;
+
+    // the output projection's bias of this lane's columns, the same for every tile
+    float bv[PAIRS][8];
+#pragma unroll
+    for (int pp = 0; pp < PAIRS; ++pp) {
+        const int col = col0 + 32 * (wave + pp * TW) + 8 * g;
+        half8 b8 = fzero8();
+        if constexpr (!LN) b8 = fld8(a.b + col);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bv[pp][j] = (float)b8[j];
+    }
+
+    // rows of tile t (rows past M repeat the last row; their outputs are never stored)
+    RowTile<K, kTileRows, TH> xt;
+    const auto fetch = [&](int t) {
+        constexpr int TPR = RowTile<K, kTileRows, TH>::kTPR;
+        const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+        const int m = min(t * kTileRows + row, a.M - 1);
+#pragma unroll
+        for (int j = 0; j < RowTile<K, kTileRows, TH>::kChunks; ++j)
+            xt.v[j] = fld8(a.x + (int64_t)m * K + 8 * (part + TPR * j));
+    };
+
+    const auto body = [&](int tile, auto full_tag) {
+        constexpr bool kFull = decltype(full_tag)::value;
+        const int m0 = tile * kTileRows;
+        // this tile's residual, loaded before the next tile's rows so that waiting for it does
+        // not wait for them
+        half8 res[PAIRS][4];
+        if (!LN && a.residual != nullptr) {
+#pragma unroll
+            for (int pp = 0; pp < PAIRS; ++pp)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    const int row = min(m0 + 16 * rb + r16, a.M - 1);
+                    res[pp][rb] = fld8(a.residual + (int64_t)row * a.n + col0 + 32 * (wave + pp * TW) + 8 * g);
+                }
+        }
+        __syncthreads();  // the previous tile's operand reads are done
+        ln_rows_to_frags<K, kTileRows, false, LN>(Xf, xt, sc, of, a.eps);
+        __syncthreads();
+        fetch(min(tile + (int)gridDim.x, tiles - 1));
+
+        half8 xop[4][KS];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
+
+#pragma unroll
+        for (int pp = 0; pp < PAIRS; ++pp) {
+            const int cp = wave + pp * TW;
+            float4v acc[2][4];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    const half8 w = fld8(Wf + frag(2 * cp + hb, ks, KS, lane));
+#pragma unroll
+                    for (int rb = 0; rb < 4; ++rb) acc[hb][rb] = mfma16x16x32(w, xop[rb][ks], acc[hb][rb]);
+                }
+            }
+            const int col = col0 + 32 * cp + 8 * g;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int row = m0 + 16 * rb + r16;
+                if (!kFull && row >= a.M) continue;
+                half8 o;
+                if constexpr (LN) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = (half_t)acc[j >> 2][rb][j & 3];
+                } else if (a.residual != nullptr) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[pp][j] + (float)res[pp][rb][j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[pp][j]);
+                }
+                fst8(a.out + (int64_t)row * a.n + col, o);
+            }
+        }
+        if (heads_wave) {
+            // the head-bias block reads every row block
+            float4v acc[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) acc[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 w = fld8(Hf + frag(0, ks, KS, lane));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acc[rb] = mfma16x16x32(w, xop[rb][ks], acc[rb]);
+            }
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int row = m0 + 16 * rb + r16;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int h = 4 * g + i;
+                    if (h < a.heads && (kFull || row < a.M)) a.bias[(int64_t)h * a.M + row] = (half_t)acc[rb][i];
+                }
+            }
+        }
+    };
+
+    // the first whole tile runs before the loop, so that the loop is entered, like every later
+    // iteration, with a tile's stores issued after the rows it prefetched
+    int tile = blockIdx.x;
+    if (tile < tiles) fetch(tile);
+    if (tile < full) {
+        body(tile, std::true_type{});
+        tile += gridDim.x;
+    }
+    for (; tile < full; tile += gridDim.x) body(tile, std::true_type{});
+    if (tile < tiles) body(tile, std::false_type{});
 }
 
 // ---- ln_gated_dual_proj ---------------------------------------------------------------------
@@ -971,10 +1126,27 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     const size_t lds = (size_t)(std::min(a.cols, std::max(a.n, 0)) * K) * 2 + fixed;
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     const dim3 grid(persistent_grid(tiles, lds), chunks);
-    constexpr int TH = kProjThreads;
-    if (int st = launch_fused(what, proj_kernel<K, LN, TH>, grid, lds, s, &a, 0)) return st;
+    constexpr int TH = kProjThreads, TW = TH / kWave;
+    // the fixed-shape kernel: no keep mask, and every column chunk a whole number (1 or 2) of
+    // column pairs per wave
+    const int pairs = a.cols / 32;
+    const bool fast = a.keep == nullptr && a.n % a.cols == 0 && pairs % TW == 0 &&
+                      (pairs / TW == 1 || pairs / TW == 2);
+    if (fast && pairs / TW == 1) {
+        if (int st = launch_fused(what, proj_fast_kernel<K, LN, TH, 1>, grid, lds, s, &a, 0)) return st;
+    } else if (fast) {
+        if (int st = launch_fused(what, proj_fast_kernel<K, LN, TH, 2>, grid, lds, s, &a, 0)) return st;
+    } else {
+        if (int st = launch_fused(what, proj_kernel<K, LN, TH>, grid, lds, s, &a, 0)) return st;
+    }
     stage_mark(s, 0);
-    hipLaunchKernelGGL((proj_kernel<K, LN, TH>), grid, dim3(TH), lds, s, a);
+    if (fast && pairs / TW == 1) {
+        hipLaunchKernelGGL((proj_fast_kernel<K, LN, TH, 1>), grid, dim3(TH), lds, s, a);
+    } else if (fast) {
+        hipLaunchKernelGGL((proj_fast_kernel<K, LN, TH, 2>), grid, dim3(TH), lds, s, a);
+    } else {
+        hipLaunchKernelGGL((proj_kernel<K, LN, TH>), grid, dim3(TH), lds, s, a);
+    }
     stage_mark(s, 1);
     return launch_status(what);
 }
