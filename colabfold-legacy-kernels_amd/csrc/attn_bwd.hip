@@ -38,8 +38,9 @@ struct BwdArgs {
     half_t* dk;
     half_t* dv;
     float* dbias;
-    float* delta;    // workspace [N, H, SqA]: -rowsum(out * dout), 0 past Sq
-    float* lse2p;    // workspace [N, H, SqA]: -lse / c1, -inf past Sq
+    // workspace [N, H, SqA / 32][64]: per 32-query tile, -lse2 / c1 of its queries (-inf past
+    // Sq), then -rowsum(out * dout) of them (0 past Sq)
+    float* qstat;
     half_t* biast;   // workspace [H, SkA, SqA]: bias[h][q][key], 0 outside
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
     int N, H, Sq, Sk, D;
@@ -151,8 +152,9 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
         if (gq < a.SqA && g == 0) {
             // the dK/dV kernel's accumulator inputs: -delta and -lse2 / c1 (past Sq the latter
             // is infinite with the sign that makes c1 times it -inf)
-            a.delta[nh * a.SqA + gq] = in ? -dlt[qb] : 0.f;
-            a.lse2p[nh * a.SqA + gq] = (in ? -lse2[qb] : -INFINITY) / a.c1;
+            float* st = a.qstat + (nh * a.SqA + (gq & ~31)) * 2 + (gq & 31);
+            st[0] = (in ? -lse2[qb] : -INFINITY) / a.c1;
+            st[32] = in ? -dlt[qb] : 0.f;
         }
     }
 
@@ -333,21 +335,44 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 // the masked logit in place of its bias, so p still carries dV; its dS is set to 0. Both happen
 // on a path that only waves holding a dead key take.
 // ------------------------------------------------------------------------------------------
+// LDS layout of the dK/dV kernel's Q and dO tiles (32 rows of DP halfs), in 4-byte words: panels
+// of 32 columns, 512 words each; in a panel LDS row R takes 16 words, with its 16-byte chunk k at
+// chunk k ^ 2 (m / 2) and the 8-byte half h of a chunk at half h ^ (m % 2), m = (R / 4) % 4.
+// gfx950's LDS serves 8-byte reads 32 lanes at a time from 64 banks; with this layout the
+// kernel's two 8-byte read shapes, 16 rows of one chunk (the row-form A operands, two reads)
+// and 8 rows x 4 chunks (the transpose reads), fall on distinct banks. `col` is a multiple of 4.
+__device__ __forceinline__ int dkdv_word(int R, int col) {
+    const int p = col >> 5, k = (col >> 3) & 3, h = (col >> 2) & 1, m = (R >> 2) & 3;
+    return 512 * p + 16 * R + 4 * (k ^ (2 * (m >> 1))) + 2 * (h ^ (m & 1));
+}
+
+// The transposed MFMA operand of d block db from a tile in that layout: A row r of the block is
+// d = 32 (db / 2) + 8 (r / 4) + 4 (db % 2) + r % 4, its k-slot j tile row 8 g + j (at LDS row
+// perm_row(8 g + j, 8)); two transpose reads of 4 rows each.
+__device__ __forceinline__ half8 dkdv_operand_tr(const half_t* tile, int g, int lane16, int db) {
+    const int j = lane16 >> 2, c = lane16 & 3;
+    const int col = 32 * (db >> 1) + 4 * (db & 1) + 8 * c;
+    const half4 lo = lds_read_tr16(tile + 2 * dkdv_word(perm_row(8 * g + j, 8), col));
+    const half4 hi = lds_read_tr16(tile + 2 * dkdv_word(perm_row(8 * g + 4 + j, 8), col));
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 template <int DP, int QG>
 struct DkdvTile {
     static constexpr int kWaves = 4 * QG, kThreads = kWaves * kWave;
     static constexpr int kBK = 64;                    // keys per workgroup, 16 per key group
     static constexpr int kBQ = 32;                    // queries per tile (one contraction step)
     static constexpr int kKS = DP / 32, kDB = DP / 16;
-    static constexpr int kLd = DP + 8;
+    static constexpr int kTile = kBQ * DP;            // halfs of a Q or dO tile
     static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO chunks of one tile
     static constexpr int kCPT = (kChunks + 255) / 256;
-    // halfs per row group and buffer: Q and dO rows, then the tile's -lse2 / c1 and -delta
-    static constexpr int kRowsHalfs = 2 * kBQ * kLd;
+    // halfs per row group and buffer: the Q tile, 128 bytes of gap, the dO tile, then the tile's
+    // -lse2 / c1 and -delta (the gap keeps the compiler from pairing a Q read with the dO read at
+    // the same offset into one two-address read, whose halves would then need register moves)
+    static constexpr int kOs = kTile + 64;
+    static constexpr int kRowsHalfs = kOs + kTile;
     static constexpr int kStage = kRowsHalfs + 2 * kBQ * 2;
     static constexpr int kStageBytes = kStage * 2 * 2 * QG;  // two buffers per row group
-    // dBias partial [kBK keys][SqA + kDBPad]: the pad staggers the keys' rows across LDS banks
-    static constexpr int kDBPad = 4;
 };
 
 template <int DP, int QG, bool DBIAS>
@@ -361,7 +386,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int c = rest % a.chunks, h = rest / a.chunks;
     const int n_begin = c * a.chunk;
     const int n_end = min(a.N, n_begin + a.chunk);
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    // the wave index as a scalar: a row group's rows, tiles and step decisions are then uniform
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int kg = wave & 3, rg = wave >> 2, gtid = tid & 255;
     const int r16 = lane & 15, g = lane >> 4;
     const int klocal = kg * 16 + r16;
@@ -371,80 +398,106 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int qsteps = (qtiles + 1) & ~1;            // steps per row: even, an odd count padded
     const int stagger = qtiles / QG;                 // tile offset between row groups
     const int rows = (n_end - n_begin + QG - 1) / QG;  // row passes of the busiest row group
-    const int total = rows * qsteps;
 
     half_t* const stage0 = reinterpret_cast<half_t*>(lds_raw) + rg * T::kStage;
     constexpr int kBufStride = QG * T::kStage;  // halfs from buffer 0 to buffer 1 of a group
-    const int dbld = a.SqA + T::kDBPad;
-    float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);  // [kBK][dbld]
+    // dBias partial [SqA / 4][kBK keys][4 queries]: a 16-lane group's four queries of 16 keys
+    // are one contiguous 256 bytes
+    float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);
 
     if constexpr (DBIAS) {
-        for (int i = tid; i < T::kBK * dbld; i += T::kThreads) DBt[i] = 0.f;
+        for (int i = tid; i < T::kBK * a.SqA; i += T::kThreads) DBt[i] = 0.f;
     }
 
     const float scale = a.scale;
     const float c1s = a.c1s;  // scale, or the stand-in for a negligible scale (K is zero then)
-    const half_t* bt_own = a.biast + ((int64_t)h * a.SkA + key) * a.SqA + 8 * g;
 
-    // Step t of this row group is query tile tile_of(t % qsteps) of row row_of(t); a step past
-    // the row's tiles, or of a row past n_end, is idle. Every load below is issued
-    // unconditionally from a valid (clamped) address and judged only where it is used, so the
-    // loop body is straight-line and each wait covers exactly the loads it needs.
-    const auto row_of = [&](int t) { return n_begin + rg + QG * (t / qsteps); };
+    // Step `it` of a row pass is query tile tile_of(it) of the group's row for that pass; a step
+    // past the row's tiles, or a pass past n_end, is idle. Every load below is issued
+    // unconditionally, from a scalar base and a lane offset fixed for the kernel, and judged
+    // only where it is used, so the loop body is straight-line and each wait covers exactly the
+    // loads it needs.
     const auto tile_of = [&](int it) {
         const int x = (it < qtiles ? it : 0) + rg * stagger;
         return x >= qtiles ? x - qtiles : x;
     };
+    // This lane's Q / dO chunks of a tile: a fixed row and column of a fixed source, Q or dO,
+    // that is the same across a wave. The chunks are read with buffer loads whose range is the
+    // tile's rows below Sq, so a row past Sq, a column past D and an idle step all read zeros.
+    uint32_t cvoff[T::kCPT];
+    int cdst0[T::kCPT], cdst1[T::kCPT];  // LDS halfs of the chunk's two 8-byte halves
+    bool cdo[T::kCPT];
+#pragma unroll
+    for (int i = 0; i < T::kCPT; ++i) {
+        const int cc = gtid + i * 256;  // every (Q, dO) x row x column chunk: kChunks = 256 kCPT
+        const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
+        const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
+        cvoff[i] = col < a.D ? (uint32_t)((row * a.D + col) * 2) : 0x80000000u;
+        cdst0[i] = which * T::kOs + 2 * dkdv_word(perm_row(row, 8), col);
+        cdst1[i] = which * T::kOs + 2 * dkdv_word(perm_row(row, 8), col + 4);
+        cdo[i] = (64 * (wave & 3) + 256 * i) / (T::kBQ * DP / 8) != 0;  // 4 DP is a multiple of 64
+    }
+    // the tile's query terms: [-lse2 / c1 of its 32 queries][-delta of them], 16 bytes a lane
+    const uint32_t st_off = 16u * (uint32_t)(gtid & 15);
+    // this lane's eight queries' bias at its key
+    const char* const bt_base =
+        reinterpret_cast<const char*>(a.biast + ((int64_t)h * a.SkA + kblk * T::kBK) * a.SqA);
+    const uint32_t bt_off = (uint32_t)(klocal * a.SqA + 8 * g) * 2u;
 
-    // A step's Q / dO chunks with their in-range bits, and the tile's -lse2 / c1 and -delta (one
-    // float4 per lane; lanes 0..15 of the group stage them): two register sets, one per step
-    // parity, fetched two steps ahead of their stage. This lane's eight queries' bias at its key:
-    // two register sets likewise, two steps ahead of their use. (Padded past Sq: -lse2 / c1
-    // infinite, -delta 0, bias 0.)
+    // A step's Q / dO chunks and query terms: two register sets, one per step parity, fetched
+    // two steps ahead of their stage. The bias: two register sets likewise, two steps ahead of
+    // their use. (Padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0.)
     struct Chunks {
         half8 s[T::kCPT];
-        uint32_t ok;
         float4v st;
     };
     Chunks ch0, ch1;
     half8 bt0, bt1;
-    const auto fetch_s = [&](Chunks& d, int t) {
-        const int n = row_of(t), it = t % qsteps, q0 = tile_of(it) * T::kBQ;
-        const bool nv = n < n_end && it < qtiles;
-        const int64_t nh = (int64_t)(nv ? n : n_begin) * a.H + h, base = nh * a.Sq * a.D;
-        d.ok = 0u;
+    // The chunk and bias prefetches walk the steps with cursors of their own, ahead of the
+    // step being computed; a cursor past the last pass reads zeros (chunks) or a valid tile
+    // (bias), unused.
+    int cs_pass = 0, cs_it = 0, cs_tile = tile_of(0);
+    bool cs_rowv = false;
+    const char *cs_q = nullptr, *cs_o = nullptr, *cs_st = nullptr;
+    const auto cs_row = [&]() {
+        const int n = n_begin + rg + QG * cs_pass;
+        cs_rowv = n < n_end;
+        const int64_t nh = (int64_t)(cs_rowv ? n : n_begin) * a.H + h;
+        cs_q = reinterpret_cast<const char*>(a.q + nh * a.Sq * a.D);
+        cs_o = reinterpret_cast<const char*>(a.dout + nh * a.Sq * a.D);
+        cs_st = reinterpret_cast<const char*>(a.qstat + nh * a.SqA * 2);
+    };
+    const auto fetch_s = [&](Chunks& d) {
+        const int q0 = cs_tile * T::kBQ;
+        const bool v = cs_rowv && cs_it < qtiles;
+        const int bytes = v ? min(T::kBQ, a.Sq - q0) * a.D * 2 : 0;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int cc = gtid + i * 256;  // every (Q, dO) x row x column chunk: kChunks = 256 kCPT
-            const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
-            const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
-            const bool ok = nv && q0 + row < a.Sq && col < a.D;
-            const half_t* src = which ? a.dout : a.q;
-            const int qr = q0 + row < a.Sq ? q0 + row : a.Sq - 1;
-            d.s[i] = bld8(src + base + (int64_t)qr * a.D + (col < a.D ? col : 0));
-            d.ok |= (uint32_t)ok << i;
+            const char* src = (cdo[i] ? cs_o : cs_q) + q0 * a.D * 2;
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(src), 0, bytes, 0x00020000);
+            d.s[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff[i], 0, 0));
         }
-        const int l16 = gtid & 15;
-        const float* src = (l16 < 8 ? a.lse2p : a.delta) + nh * a.SqA + q0 + 4 * (l16 & 7);
-        d.st = *reinterpret_cast<const float4v*>(src);
+        d.st = *reinterpret_cast<const float4v*>(cs_st + q0 * 8 + st_off);
+        if (++cs_it == qsteps) {
+            cs_it = 0;
+            ++cs_pass;
+            cs_row();
+        }
+        cs_tile = tile_of(cs_it);
     };
-    const auto fetch_c = [&](half8& d, int t) { d = bld8(bt_own + tile_of(t % qsteps) * T::kBQ); };
+    int bc_it = 0;
+    const auto fetch_c = [&](half8& d) {
+        d = *reinterpret_cast<const half8*>(bt_base + tile_of(bc_it) * (T::kBQ * 2) + bt_off);
+        if (++bc_it == qsteps) bc_it = 0;
+    };
     const auto stage_tile = [&](const Chunks& d, int buf) {
         half_t* Qs = stage0 + buf * kBufStride;
-        half_t* Os = Qs + T::kBQ * T::kLd;
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int cc = gtid + i * 256;
-            const int which = cc / (T::kBQ * DP / 8), w = cc - which * (T::kBQ * DP / 8);
-            const int row = w / (DP / 8), col = (w - row * (DP / 8)) * 8;
-            half_t* rm = which ? Os : Qs;
-            *reinterpret_cast<half8*>(&rm[perm_row(row, 8) * T::kLd + col]) =
-                (d.ok >> i) & 1u ? d.s[i] : bzero8();
+            *reinterpret_cast<half4*>(Qs + cdst0[i]) = half4{d.s[i][0], d.s[i][1], d.s[i][2], d.s[i][3]};
+            *reinterpret_cast<half4*>(Qs + cdst1[i]) = half4{d.s[i][4], d.s[i][5], d.s[i][6], d.s[i][7]};
         }
-        if (gtid < 16) {
-            // [-lse2 / c1 of the 32 queries][-delta of the 32 queries]
-            *reinterpret_cast<float4v*>(reinterpret_cast<float*>(Qs + T::kRowsHalfs) + 4 * gtid) = d.st;
-        }
+        if (gtid < 16) *reinterpret_cast<float4v*>(reinterpret_cast<float*>(Qs + T::kRowsHalfs) + 4 * gtid) = d.st;
     };
 
     // K and V of this group's next row as the B operands (lane column = key, slots
@@ -470,32 +523,34 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     bool alive = false, all_alive = true, nv = false;
     float4v accv[T::kDB], acck[T::kDB];
 
-    if (total > 0) {
+    cs_row();
+    if (rows > 0) {
         fetch_kv(0);
-        fetch_s(ch0, 0);
-        fetch_s(ch1, min(1, total - 1));
-        fetch_c(bt0, 0);
-        fetch_c(bt1, min(1, total - 1));
+        fetch_s(ch0);
+        fetch_s(ch1);
+        fetch_c(bt0);
+        fetch_c(bt1);
         stage_tile(ch0, 0);
-        fetch_s(ch0, min(2, total - 1));
+        fetch_s(ch0);
     }
     __syncthreads();
 
-    // step t reads LDS buffer t & 1 and the bias set of its parity, which it refills with step
-    // t + 2 once consumed; at its end it stages step t + 1 from the chunk set of that parity and
-    // refills the set with step t + 3 (steps past the end load the last step again, unused)
-    const auto step = [&](int t, Chunks& next, half8& bt) {
-        const int buf = t & 1, it = t % qsteps, q0 = tile_of(it) * T::kBQ;
+    // step (pass, it) reads LDS buffer it & 1 and the bias set of its parity, which it refills
+    // with the step two on once consumed; at its end it stages the next step from the chunk set
+    // of that parity and refills the set with the step three on (steps past the end load the
+    // last step again, unused)
+    const auto step = [&](int it, Chunks& next, half8& bt) {
+        const int buf = it & 1, q0 = tile_of(it) * T::kBQ;
         const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
-        const half_t* Os = Qs + T::kBQ * T::kLd;
+        const half_t* Os = Qs + T::kOs;
         const float* Ls = reinterpret_cast<const float*>(Qs + T::kRowsHalfs);  // -lse2 / c1, -delta
 
         // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
         // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
-        float x[8];
-        float4v dp[2];
         if (valid) {
+            float x[8];
+            float4v dp[2];
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 const int qrow = 16 * qb + r16;
@@ -503,22 +558,27 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 dp[qb] = *reinterpret_cast<const float4v*>(Ls + T::kBQ + 8 * g + 4 * qb);
 #pragma unroll
                 for (int ks = 0; ks < T::kKS; ++ks) {
-                    const half8 qa = bld8(&Qs[qrow * T::kLd + 32 * ks + 8 * g]);
-                    const half8 oa = bld8(&Os[qrow * T::kLd + 32 * ks + 8 * g]);
+                    const int w0 = 2 * dkdv_word(qrow, 32 * ks + 8 * g);
+                    const int w1 = 2 * dkdv_word(qrow, 32 * ks + 8 * g + 4);
+                    const half4 q0v = *reinterpret_cast<const half4*>(Qs + w0);
+                    const half4 q1v = *reinterpret_cast<const half4*>(Qs + w1);
+                    const half4 o0v = *reinterpret_cast<const half4*>(Os + w0);
+                    const half4 o1v = *reinterpret_cast<const half4*>(Os + w1);
+                    const half8 qa = half8{q0v[0], q0v[1], q0v[2], q0v[3], q1v[0], q1v[1], q1v[2], q1v[3]};
+                    const half8 oa = half8{o0v[0], o0v[1], o0v[2], o0v[3], o1v[0], o1v[1], o1v[2], o1v[3]};
                     s = mfma16x16x32(qa, kop[ks], s);
                     dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
                 }
-                // s2 = log2e (scale S + bias), a dead key's bias being the masked logit
+                // s2 = log2e (scale S + bias); a dead key (K zero) takes the masked logit
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const half_t b = all_alive || alive ? bt[4 * qb + i] : (half_t)kMaskedLogit;
-                    x[4 * qb + i] = fmaf(s[i], c1s, (float)b) * kLog2e;
+                for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1s, (float)bt[4 * qb + i]) * kLog2e;
+                if (!all_alive) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        x[4 * qb + i] = alive ? x[4 * qb + i] : fmaf(s[i], c1s, kMaskedLogit) * kLog2e;
+                    }
                 }
             }
-        }
-        fetch_c(bt, min(t + 2, total - 1));  // the bias two steps on, into the registers just consumed
-
-        if (valid) {
             half8 pb, dsb;
             float dsf[8];
 #pragma unroll
@@ -538,30 +598,29 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 // the row groups' tiles are disjoint at every step, and this lane is the only
                 // writer of these eight elements within its group (a read-modify-write: LDS float
                 // atomics measured several times slower here)
-                float* row = DBt + klocal * dbld + q0 + 8 * g;
+                float* row = DBt + (q0 / 4 + 2 * g) * (4 * T::kBK) + 4 * klocal;
                 float4 lo = *reinterpret_cast<float4*>(row);
-                float4 hi = *reinterpret_cast<float4*>(row + 4);
+                float4 hi = *reinterpret_cast<float4*>(row + 4 * T::kBK);
                 lo.x += dsf[0]; lo.y += dsf[1]; lo.z += dsf[2]; lo.w += dsf[3];
                 hi.x += dsf[4]; hi.y += dsf[5]; hi.z += dsf[6]; hi.w += dsf[7];
                 *reinterpret_cast<float4*>(row) = lo;
-                *reinterpret_cast<float4*>(row + 4) = hi;
+                *reinterpret_cast<float4*>(row + 4 * T::kBK) = hi;
             }
 
-            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4,
-            // its k-slots queries 8 g + j, read transposed from the row-major tiles
-            const auto orow = [&](int r) { return Os + perm_row(r, 8) * T::kLd; };
-            const auto qrow = [&](int r) { return Qs + perm_row(r, 8) * T::kLd; };
+            // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is
+            // d = 32 (db/2) + 8 (r/4) + 4 (db%2) + r%4, its k-slots queries 8 g + j, read transposed
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
-                const half8 ot = lds_operand_tr(orow, g, r16, 4 * db, DP / 4);
-                const half8 qt = lds_operand_tr(qrow, g, r16, 4 * db, DP / 4);
+                const half8 ot = dkdv_operand_tr(Os, g, r16, db);
+                const half8 qt = dkdv_operand_tr(Qs, g, r16, db);
                 accv[db] = mfma16x16x32(ot, pb, accv[db]);
                 acck[db] = mfma16x16x32(qt, dsb, acck[db]);
             }
         }
+        fetch_c(bt);  // the bias two steps on, into the registers just consumed
         // the other buffer was last read a step ago, before the barrier that ended that step
         stage_tile(next, buf ^ 1);
-        fetch_s(next, min(t + 3, total - 1));
+        fetch_s(next);  // the chunks three steps on
         __syncthreads();
     };
 
@@ -583,16 +642,16 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         fetch_kv(pass + 1 < rows ? pass + 1 : pass);
 
         for (int it = 0; it < qsteps; it += 2) {
-            step(pass * qsteps + it, ch1, bt0);
-            step(pass * qsteps + it + 1, ch0, bt1);
+            step(it, ch1, bt0);
+            step(it + 1, ch0, bt1);
         }
 
         if (nv && kin) {
-            // the row is done: lane holds d = (DP/4) g .. +DP/4 of its key
+            // the row is done: lane holds d = 32 cc + 8 g .. + 8 of its key for each panel cc
             const int64_t off = ((int64_t)n * a.H + h) * a.Sk * a.D + (int64_t)key * a.D;
 #pragma unroll
             for (int cc = 0; cc < DP / 32; ++cc) {
-                const int d0 = (DP / 4) * g + 8 * cc;
+                const int d0 = 32 * cc + 8 * g;
                 if (d0 >= a.D) continue;
                 half8 ok, ov;
 #pragma unroll
@@ -609,7 +668,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     if constexpr (DBIAS) {
         float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * T::kBK;
         for (int i = tid; i < a.SqA * T::kBK; i += T::kThreads) {
-            dst[i] = DBt[(i % T::kBK) * dbld + i / T::kBK];  // to [SqA][64]
+            const int q = i / T::kBK, kk = i % T::kBK;
+            dst[i] = DBt[(q >> 2) * (4 * T::kBK) + 4 * kk + (q & 3)];  // to [SqA][64]
         }
     }
 }
@@ -744,7 +804,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.SqA = (int)(((Sq + 31) / 32) * 32);
     p.kblocks = (int)((Sk + 63) / 64);
     p.SkA = p.kblocks * 64;
-    p.dbias_lds = (size_t)64 * (p.SqA + 4) * sizeof(float);  // the dK/dV kernel's [64][SqA + 4]
+    p.dbias_lds = (size_t)64 * p.SqA * sizeof(float);  // the dK/dV kernel's dBias partial
     const int limit = shared_limit(device);
     // row groups of the dK/dV kernel: at most the query tiles of a row, which they walk from
     // staggered starts
@@ -790,7 +850,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     }
     p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
-    p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // delta, and lse2 after it
+    p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // half of the query terms
     p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(half_t));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     return p;
@@ -918,8 +978,7 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.dv = static_cast<half_t*>(dv->data);
     a.dbias = static_cast<float*>(dbias->data);
     char* ws = static_cast<char*>(workspace);
-    a.delta = reinterpret_cast<float*>(ws);
-    a.lse2p = reinterpret_cast<float*>(ws + p.delta_bytes);
+    a.qstat = reinterpret_cast<float*>(ws);
     a.biast = reinterpret_cast<half_t*>(ws + 2 * p.delta_bytes);
     a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
