@@ -330,7 +330,8 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 // step, in an order fixed by the schedule.
 //
 // The per-query terms enter the MFMAs as accumulator inputs: S starts from -lse2 / (scale log2e)
-// and dP from -delta (both staged in LDS with the tile), so that s2 = scale log2e S + bias log2e
+// and dP from -delta (a lane loads one of its 16-lane row's sixteen terms with the tile's chunks
+// and the row shares them by DPP broadcasts), so that s2 = scale log2e S + bias log2e
 // is one fma and dS = p dP one multiply. A dead key (masked, or past Sk) has zero K and V rows and
 // the masked logit in place of its bias, so p still carries dV; its dS is set to 0. Both happen
 // on a path that only waves holding a dead key take.
@@ -357,6 +358,16 @@ __device__ __forceinline__ half8 dkdv_operand_tr(const half_t* tile, int g, int 
     return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Lanes B .. B + 3 of this lane's 16-lane row (DPP row broadcasts).
+template <int B>
+__device__ __forceinline__ float4v row_quad(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    return float4v{__builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x150 + B, 0xf, 0xf, true)),
+                   __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x151 + B, 0xf, 0xf, true)),
+                   __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x152 + B, 0xf, 0xf, true)),
+                   __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x153 + B, 0xf, 0xf, true))};
+}
+
 template <int DP, int QG>
 struct DkdvTile {
     static constexpr int kWaves = 4 * QG, kThreads = kWaves * kWave;
@@ -366,12 +377,11 @@ struct DkdvTile {
     static constexpr int kTile = kBQ * DP;            // halfs of a Q or dO tile
     static constexpr int kChunks = 2 * kBQ * DP / 8;  // Q and dO chunks of one tile
     static constexpr int kCPT = (kChunks + 255) / 256;
-    // halfs per row group and buffer: the Q tile, 128 bytes of gap, the dO tile, then the tile's
-    // -lse2 / c1 and -delta (the gap keeps the compiler from pairing a Q read with the dO read at
-    // the same offset into one two-address read, whose halves would then need register moves)
+    // halfs per row group and buffer: the Q tile, 128 bytes of gap, then the dO tile (the gap
+    // keeps the compiler from pairing a Q read with the dO read at the same offset into one
+    // two-address read, whose halves would then need register moves)
     static constexpr int kOs = kTile + 64;
-    static constexpr int kRowsHalfs = kOs + kTile;
-    static constexpr int kStage = kRowsHalfs + 2 * kBQ * 2;
+    static constexpr int kStage = kOs + kTile;
     static constexpr int kStageBytes = kStage * 2 * 2 * QG;  // two buffers per row group
 };
 
@@ -437,8 +447,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         cdst1[i] = which * T::kOs + 2 * dkdv_word(perm_row(row, 8), col + 4);
         cdo[i] = (64 * (wave & 3) + 256 * i) / (T::kBQ * DP / 8) != 0;  // 4 DP is a multiple of 64
     }
-    // the tile's query terms: [-lse2 / c1 of its 32 queries][-delta of them], 16 bytes a lane
-    const uint32_t st_off = 16u * (uint32_t)(gtid & 15);
+    // one of the tile's query terms, [-lse2 / c1 of its 32 queries][-delta of them]: lane i of
+    // 16-lane row g holds -lse2 / c1 of query 8 g + i for i < 8, -delta of query 8 g + i - 8 above
+    const uint32_t st_off = 4u * (uint32_t)(r16 < 8 ? 8 * g + r16 : T::kBQ + 8 * g + r16 - 8);
     // this lane's eight queries' bias at its key
     const char* const bt_base =
         reinterpret_cast<const char*>(a.biast + ((int64_t)h * a.SkA + kblk * T::kBK) * a.SqA);
@@ -449,9 +460,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     // their use. (Padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0.)
     struct Chunks {
         half8 s[T::kCPT];
-        float4v st;
+        float st;
     };
     Chunks ch0, ch1;
+    float stc = 0.f;  // the staged step's query term
     half8 bt0, bt1;
     // The chunk and bias prefetches walk the steps with cursors of their own, ahead of the
     // step being computed; a cursor past the last pass reads zeros (chunks) or a valid tile
@@ -477,7 +489,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(src), 0, bytes, 0x00020000);
             d.s[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff[i], 0, 0));
         }
-        d.st = *reinterpret_cast<const float4v*>(cs_st + q0 * 8 + st_off);
+        d.st = *reinterpret_cast<const float*>(cs_st + q0 * 8 + st_off);
         if (++cs_it == qsteps) {
             cs_it = 0;
             ++cs_pass;
@@ -497,7 +509,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             *reinterpret_cast<half4*>(Qs + cdst0[i]) = half4{d.s[i][0], d.s[i][1], d.s[i][2], d.s[i][3]};
             *reinterpret_cast<half4*>(Qs + cdst1[i]) = half4{d.s[i][4], d.s[i][5], d.s[i][6], d.s[i][7]};
         }
-        if (gtid < 16) *reinterpret_cast<float4v*>(reinterpret_cast<float*>(Qs + T::kRowsHalfs) + 4 * gtid) = d.st;
+        stc = d.st;
     };
 
     // K and V of this group's next row as the B operands (lane column = key, slots
@@ -544,7 +556,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
         const half_t* Os = Qs + T::kOs;
-        const float* Ls = reinterpret_cast<const float*>(Qs + T::kRowsHalfs);  // -lse2 / c1, -delta
 
         // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
         // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
@@ -554,8 +565,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 const int qrow = 16 * qb + r16;
-                float4v s = *reinterpret_cast<const float4v*>(Ls + 8 * g + 4 * qb);
-                dp[qb] = *reinterpret_cast<const float4v*>(Ls + T::kBQ + 8 * g + 4 * qb);
+                float4v s = qb == 0 ? row_quad<0>(stc) : row_quad<4>(stc);
+                dp[qb] = qb == 0 ? row_quad<8>(stc) : row_quad<12>(stc);
 #pragma unroll
                 for (int ks = 0; ks < T::kKS; ++ks) {
                     const int w0 = 2 * dkdv_word(qrow, 32 * ks + 8 * g);
