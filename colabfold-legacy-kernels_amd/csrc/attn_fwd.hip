@@ -33,7 +33,6 @@ struct FwdArgs {
     int N, H, Sq, Sk, D;
     float scale;
     int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0)
-    int mask_vec;  // mask rows are whole 16-byte vectors (Sk % 16 == 0)
     int head_major;  // work items head-major ([N,H,S,D] tensors), else row-major (packed rows)
 };
 
@@ -79,17 +78,6 @@ __device__ __forceinline__ H16 load_h16(const half_t* p, int valid, bool vec) {
         }
     }
     return r;
-}
-
-// 16 consecutive mask bytes as four little-endian words, bytes at or past `valid` as 0
-__device__ __forceinline__ uint4 load_m16(const uint8_t* p, int valid, bool vec) {
-    if (vec && valid >= 16) return *reinterpret_cast<const uint4*>(p);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (j < valid) w[j / 4] |= (uint32_t)(p[j] != 0) << (8 * (j % 4));
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 template <int DP, bool LSE, bool GATE, bool TRIM>
@@ -155,91 +143,101 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         for (int db = 0; db < T::kDB; ++db) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
+    const float scale = a.scale;
 
-    // K/V tile chunks held in registers one tile ahead of their LDS store, with their key's raw
-    // mask byte: a masked key's K row is staged as zeros, so its score is exactly 0 and its bias
-    // register (which then holds the masked logit) is its logit. Nothing loaded here is examined
-    // before the stage a tile later, so the loads stay in flight meanwhile.
+    // K/V chunks of the next key tile, held in registers one tile ahead of their LDS store. A
+    // chunk's row and column are fixed per lane; the loads are buffer loads whose range is the
+    // tile's rows below Sk, so a row past Sk and a column past D read zeros. Lane l of every wave
+    // also loads the mask byte of key k0 + l (zero past Sk): a wave ballot of those bytes is the
+    // tile's keep bits, uniform across the workgroup. A masked key's K row is staged as zeros,
+    // so its score is exactly 0 and its bias register (which then holds the masked logit) is its
+    // logit.
+    uint32_t kvoff[T::kCPT];
+    int krow[T::kCPT], kdst[T::kCPT], vdst[T::kCPT];
+#pragma unroll
+    for (int i = 0; i < T::kCPT; ++i) {
+        const int c = tid + i * T::kThreads;  // kChunks = kCPT kThreads
+        const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
+        kvoff[i] = col < a.D ? (uint32_t)((row * a.ks + col) * 2) : 0x80000000u;
+        krow[i] = row;
+        kdst[i] = perm_row(row, 16) * T::kKsLd + col;
+        vdst[i] = row * T::kKsLd + col;
+    }
+    const char* const kb_base = reinterpret_cast<const char*>(a.k + kbase);
+    const char* const vb_base = reinterpret_cast<const char*>(a.v + kbase);
+    const char* const mrow = reinterpret_cast<const char*>(a.kmask + (int64_t)n * a.Sk);
     half8 kreg[T::kCPT], vreg[T::kCPT];
-    uint32_t kmb[T::kCPT];
+    uint32_t mbyte = 0u;
     const auto fetch = [&](int k0) {
+        const int rows = min(a.Sk - k0, T::kBK);
+        const int64_t kofs = (int64_t)k0 * a.ks * 2;
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb_base + kofs), 0,
+                                                          rows * (int)a.ks * 2, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb_base + kofs), 0,
+                                                          rows * (int)a.ks * 2, 0x00020000);
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int c = tid + i * T::kThreads;
-            const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-            const bool ok = c < T::kChunks && k0 + row < a.Sk && col < a.D;
-            const int64_t off = kbase + (int64_t)(k0 + row) * a.ks + col;
-            kreg[i] = ok ? ld8(a.k + off) : zero8();
-            vreg[i] = ok ? ld8(a.v + off) : zero8();
-            kmb[i] = ok ? (uint32_t)mrow[k0 + row] : 0u;
+            kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, kvoff[i], 0, 0));
+            vreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, kvoff[i], 0, 0));
         }
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
+        mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
-    const auto stage = [&](int buf) {
+    const auto stage = [&](int buf, uint64_t keep) {
         half_t* Ks = Ks2[buf];
         half_t* Vs = Vs2[buf];
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int c = tid + i * T::kThreads;
-            if (c < T::kChunks) {
-                const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-                *reinterpret_cast<half8*>(&Ks[perm_row(row, 16) * T::kKsLd + col]) =
-                    kmb[i] != 0u ? kreg[i] : zero8();
-                *reinterpret_cast<half8*>(&Vs[row * T::kKsLd + col]) = vreg[i];
-            }
+            *reinterpret_cast<half8*>(&Ks[kdst[i]]) = (keep >> krow[i]) & 1u ? kreg[i] : zero8();
+            *reinterpret_cast<half8*>(&Vs[vdst[i]]) = vreg[i];
         }
     };
 
-    const float scale = a.scale;
-    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
-
-    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, and their raw mask bytes,
-    // one key tile ahead of their use; when the tile comes up, a masked key's bias becomes the
-    // masked logit -1e4 and a key past Sk's -inf
-    H16 bias_n[T::kQB];
-    uint4 mask_n;
-    const auto fetch_bm = [&](int k0) {
-        const int kl = k0 + 16 * g;
-        const int kvalid = a.Sk - kl;
+    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, one key tile ahead of their
+    // use, in two register sets that alternate by tile; when the tile comes up, a masked key's
+    // bias becomes the masked logit -1e4 and a key past Sk's -inf
+    const half_t* brow[T::kQB];
 #pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) {
-            const int gq = q0w + 16 * qb + r16;
-            const int gqc = gq < a.Sq ? gq : a.Sq - 1;
-            bias_n[qb] = load_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        const int gq = q0w + 16 * qb + r16;
+        const int gqc = gq < a.Sq ? gq : a.Sq - 1;
+        brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
+    }
+    const auto fetch_bias = [&](int k0, H16 (&b)[T::kQB]) {
+        if (a.bias_vec && k0 + T::kBK <= a.Sk) {
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) {
+                b[qb].lo = ld8(brow[qb] + k0);
+                b[qb].hi = ld8(brow[qb] + k0 + 8);
+            }
+        } else {
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) b[qb] = load_h16(brow[qb] + k0, a.Sk - (k0 + 16 * g), a.bias_vec);
         }
-        mask_n = load_m16(mrow + kl, kvalid, a.mask_vec);
     };
-    const auto fix_bias = [&](int k0, H16 (&b)[T::kQB], uint4 m) {
+    const auto fix_bias = [&](int k0, H16 (&b)[T::kQB], uint64_t keep64) {
         const int kvalid = a.Sk - (k0 + 16 * g);
-        const uint32_t keep = mask_bits16(m, kvalid);
+        const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
+        const uint32_t keep = (uint32_t)(keep64 >> (16 * g)) & inside;
         if (keep != 0xffffu) {
-            const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb)
-                fill_bias16(b[qb].lo, b[qb].hi, keep, inside, (half_t)kMaskedLogit,
-                            (half_t)(-INFINITY));
+                fill_bias16(b[qb].lo, b[qb].hi, keep, inside, (half_t)kMaskedLogit, (half_t)(-INFINITY));
         }
     };
 
-    if (k_end > 0) {
-        fetch(0);
-        fetch_bm(0);
-        stage(0);
-        __syncthreads();
-    }
-    for (int k0 = 0, buf = 0; k0 < k_end; k0 += T::kBK, buf ^= 1) {
+    // one key tile: prefetch the next, then S^T, the online softmax and O^T += V^T P^T
+    uint64_t keep_cur = 0u;
+    const auto tile = [&](int k0, int buf, H16 (&bias16)[T::kQB], H16 (&bias_next)[T::kQB]) {
         const half_t* Ks = Ks2[buf];
         const half_t* Vs = Vs2[buf];
         const bool more = k0 + T::kBK < k_end;
-        H16 bias16[T::kQB];
-#pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) bias16[qb] = bias_n[qb];
-        const uint4 mask16 = mask_n;
         if (more) {
             fetch(k0 + T::kBK);
-            fetch_bm(k0 + T::kBK);
+            fetch_bias(k0 + T::kBK, bias_next);
         }
-        fix_bias(k0, bias16, mask16);
+        // every key of the tile kept and inside Sk: the bias stands as loaded
+        if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
 
         // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4
         float4v s[4][T::kQB];
@@ -325,8 +323,24 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
             }
         }
         // the other buffer was last read a tile ago, before the barrier that ended that tile
-        if (more) stage(buf ^ 1);
+        if (more) {
+            keep_cur = __ballot(mbyte != 0u);
+            stage(buf ^ 1, keep_cur);
+        }
         __syncthreads();
+    };
+
+    H16 biasA[T::kQB], biasB[T::kQB];
+    if (k_end > 0) {
+        fetch(0);
+        fetch_bias(0, biasA);
+        keep_cur = __ballot(mbyte != 0u);
+        stage(0, keep_cur);
+        __syncthreads();
+    }
+    for (int k0 = 0; k0 < k_end; k0 += 2 * T::kBK) {
+        tile(k0, 0, biasA, biasB);
+        if (k0 + T::kBK < k_end) tile(k0 + T::kBK, 1, biasB, biasA);
     }
 
     // epilogue: lane g holds d = (DP/4) g .. +DP/4 of query q0w + 16 qb + r16
@@ -463,7 +477,6 @@ extern "C" int clk_attention_fwd(clk_stream stream, int32_t device, const clk_bu
     a.lse = want_lse ? static_cast<float*>(lse->data) : nullptr;
     a.scale = scale;
     a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
-    a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     return want_lse ? dispatch_fwd<true, false, false>(s, device, a)
                     : dispatch_fwd<false, false, false>(s, device, a);
@@ -518,7 +531,6 @@ static int packed_common(clk_stream stream, int32_t device, const clk_buffer* p,
     a.lse = nullptr;
     a.scale = scale;
     a.bias_vec = S % 8 == 0 && aligned16(a.bias);
-    a.mask_vec = S % 16 == 0 && aligned16(a.kmask);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (lims) {
         return G == 4 ? dispatch_fwd<false, true, true>(s, device, a)
