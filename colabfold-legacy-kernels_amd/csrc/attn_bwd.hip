@@ -52,7 +52,7 @@ struct BwdArgs {
     float c1;    // scale log2e, or 1 where |scale log2e| is below 1e-30
     float c1s;   // c1 / log2e: scale, or the stand-in's 1 / log2e
     int kscale;  // 0 where c1 stands in for a negligible scale: the dK/dV kernel's K is then zero
-    int bias_vec, mask_vec;
+    int bias_vec;
 };
 
 __device__ __forceinline__ half8 bzero8() {
@@ -81,16 +81,6 @@ __device__ __forceinline__ BH16 bload_h16(const half_t* p, int valid, bool vec) 
         }
     }
     return r;
-}
-
-__device__ __forceinline__ uint4 bload_m16(const uint8_t* p, int valid, bool vec) {
-    if (vec && valid >= 16) return *reinterpret_cast<const uint4*>(p);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        if (j < valid) w[j / 4] |= (uint32_t)(p[j] != 0) << (8 * (j % 4));
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -164,59 +154,75 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
 
-    const uint8_t* mrow = a.kmask + (int64_t)n * a.Sk;
-
-    // K/V chunks one tile ahead, with their key's raw mask byte, examined only at the stage a
-    // tile later (so the loads stay in flight); a masked key's K row is staged as zeros
+    // K/V chunks of the next key tile, one tile ahead of their LDS store: fixed row and column
+    // per lane, buffer loads whose range is the tile's rows below Sk (a row past Sk and a column
+    // past D read zeros). Lane l of every wave also loads the mask byte of key k0 + l (zero past
+    // Sk); a wave ballot of those bytes is the tile's keep bits. A masked key's K row is staged
+    // as zeros.
+    uint32_t kvoff[T::kCPT];
+    int krow[T::kCPT], kdst[T::kCPT];
+#pragma unroll
+    for (int i = 0; i < T::kCPT; ++i) {
+        const int c = tid + i * T::kThreads;  // kChunks = kCPT kThreads
+        const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
+        kvoff[i] = col < a.D ? (uint32_t)((row * a.D + col) * 2) : 0x80000000u;
+        krow[i] = row;
+        kdst[i] = perm_row(row, 16) * T::kLd + col;
+    }
+    const char* const kb_base = reinterpret_cast<const char*>(a.k + kbase);
+    const char* const vb_base = reinterpret_cast<const char*>(a.v + kbase);
+    const char* const mrow = reinterpret_cast<const char*>(a.kmask + (int64_t)n * a.Sk);
     half8 kreg[T::kCPT], vreg[T::kCPT];
-    uint32_t kmb[T::kCPT];
+    uint32_t mbyte = 0u;
     const auto fetch = [&](int k0) {
+        const int rows = min(a.Sk - k0, T::kBK);
+        const int64_t kofs = (int64_t)k0 * a.D * 2;
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb_base + kofs), 0, rows * a.D * 2, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb_base + kofs), 0, rows * a.D * 2, 0x00020000);
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int c = tid + i * T::kThreads;
-            const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-            const bool ok = c < T::kChunks && k0 + row < a.Sk && col < a.D;
-            const int64_t off = kbase + (int64_t)(k0 + row) * a.D + col;
-            kreg[i] = ok ? bld8(a.k + off) : bzero8();
-            vreg[i] = ok ? bld8(a.v + off) : bzero8();
-            kmb[i] = ok ? (uint32_t)mrow[k0 + row] : 0u;
+            kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, kvoff[i], 0, 0));
+            vreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, kvoff[i], 0, 0));
         }
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
+        mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
-    const auto stage = [&](int buf) {
+    const auto stage = [&](int buf, uint64_t keep) {
 #pragma unroll
         for (int i = 0; i < T::kCPT; ++i) {
-            const int c = tid + i * T::kThreads;
-            if (c < T::kChunks) {
-                const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
-                const half8 kv = kmb[i] != 0u ? kreg[i] : bzero8();
-                const int prow = perm_row(row, 16);
-                *reinterpret_cast<half8*>(&Ks2[buf][prow * T::kLd + col]) = kv;
-                *reinterpret_cast<half8*>(&Vs2[buf][prow * T::kLd + col]) = vreg[i];
-            }
+            *reinterpret_cast<half8*>(&Ks2[buf][kdst[i]]) = (keep >> krow[i]) & 1u ? kreg[i] : bzero8();
+            *reinterpret_cast<half8*>(&Vs2[buf][kdst[i]]) = vreg[i];
         }
     };
 
     const float scale = a.scale;
-    const int64_t bias_h = (int64_t)h * a.Sq * a.Sk;
 
-    // bias of this lane's 16 keys k0 + 16 g .. +15 and their raw mask bytes, one key tile ahead
-    // of their use; when the tile comes up, a masked key or a key past Sk gets bias -inf, so its
-    // p, and with it its dS, is 0
-    BH16 bias_n[T::kQB];
-    uint4 mask_n;
-    const auto fetch_bm = [&](int k0) {
-        const int kl = k0 + 16 * g;
-        const int kvalid = a.Sk - kl;
+    // bias of this lane's 16 keys k0 + 16 g .. +15, one key tile ahead of their use, in two
+    // register sets that alternate by tile; when the tile comes up, a masked key or a key past
+    // Sk gets bias -inf, so its p, and with it its dS, is 0
+    const half_t* brow[T::kQB];
 #pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) {
-            const int gq = q0w + 16 * qb + r16;
-            const int gqc = gq < a.Sq ? gq : a.Sq - 1;
-            bias_n[qb] = bload_h16(a.bias + bias_h + (int64_t)gqc * a.Sk + kl, kvalid, a.bias_vec);
+    for (int qb = 0; qb < T::kQB; ++qb) {
+        const int gq = q0w + 16 * qb + r16;
+        const int gqc = gq < a.Sq ? gq : a.Sq - 1;
+        brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
+    }
+    const auto fetch_bias = [&](int k0, BH16 (&b)[T::kQB]) {
+        if (a.bias_vec && k0 + T::kBK <= a.Sk) {
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) {
+                b[qb].lo = bld8(brow[qb] + k0);
+                b[qb].hi = bld8(brow[qb] + k0 + 8);
+            }
+        } else {
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) b[qb] = bload_h16(brow[qb] + k0, a.Sk - (k0 + 16 * g), a.bias_vec);
         }
-        mask_n = bload_m16(mrow + kl, kvalid, a.mask_vec);
     };
-    const auto fix_bias = [&](int k0, BH16 (&b)[T::kQB], uint4 m) {
-        const uint32_t keep = mask_bits16(m, a.Sk - (k0 + 16 * g));
+    const auto fix_bias = [&](int k0, BH16 (&b)[T::kQB], uint64_t keep64) {
+        const int kvalid = a.Sk - (k0 + 16 * g);
+        const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
+        const uint32_t keep = (uint32_t)(keep64 >> (16 * g)) & inside;
         if (keep != 0xffffu) {
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb)
@@ -224,31 +230,22 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
         }
     };
 
-    if (a.Sk > 0) {
-        fetch(0);
-        fetch_bm(0);
-        stage(0);
-        __syncthreads();
-    }
-    for (int k0 = 0, buf = 0; k0 < a.Sk; k0 += T::kBK, buf ^= 1) {
+    uint64_t keep_cur = 0u;
+    const auto tile = [&](int k0, int buf, BH16 (&bias16)[T::kQB], BH16 (&bias_next)[T::kQB]) {
         const half_t* Ks = Ks2[buf];
         const half_t* Vs = Vs2[buf];
         const bool more = k0 + T::kBK < a.Sk;
-        BH16 bias16[T::kQB];
-#pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) bias16[qb] = bias_n[qb];
-        const uint4 mask16 = mask_n;
         if (more) {
             fetch(k0 + T::kBK);
-            fetch_bm(k0 + T::kBK);
+            fetch_bias(k0 + T::kBK, bias_next);
         }
-        fix_bias(k0, bias16, mask16);
-
+        // every key of the tile kept and inside Sk: the bias stands as loaded
+        if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
 
         float4v s[4][T::kQB], dp[4][T::kQB];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const int krow = 16 * kb + r16;  // key 16 (r/4) + 4 kb + r%4
+            const int krw = 16 * kb + r16;  // key 16 (r/4) + 4 kb + r%4
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb) {
                 s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -256,8 +253,8 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
             }
 #pragma unroll
             for (int ks = 0; ks < T::kKS; ++ks) {
-                const half8 kop = bld8(&Ks[krow * T::kLd + 32 * ks + 8 * g]);
-                const half8 vop = bld8(&Vs[krow * T::kLd + 32 * ks + 8 * g]);
+                const half8 kop = bld8(&Ks[krw * T::kLd + 32 * ks + 8 * g]);
+                const half8 vop = bld8(&Vs[krw * T::kLd + 32 * ks + 8 * g]);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) {
                     s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
@@ -296,8 +293,24 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
             }
         }
         // the other buffer was last read a tile ago, before the barrier that ended that tile
-        if (more) stage(buf ^ 1);
+        if (more) {
+            keep_cur = __ballot(mbyte != 0u);
+            stage(buf ^ 1, keep_cur);
+        }
         __syncthreads();
+    };
+
+    BH16 biasA[T::kQB], biasB[T::kQB];
+    if (a.Sk > 0) {
+        fetch(0);
+        fetch_bias(0, biasA);
+        keep_cur = __ballot(mbyte != 0u);
+        stage(0, keep_cur);
+        __syncthreads();
+    }
+    for (int k0 = 0; k0 < a.Sk; k0 += 2 * T::kBK) {
+        tile(k0, 0, biasA, biasB);
+        if (k0 + T::kBK < a.Sk) tile(k0 + T::kBK, 1, biasB, biasA);
     }
 
 #pragma unroll
@@ -1004,7 +1017,6 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     if (!a.kscale) a.c1 = 1.f;  // scale log2e S is below fp32 resolution against the bias
     a.c1s = a.c1 / kLog2e;
     a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
-    a.mask_vec = Sk % 16 == 0 && aligned16(a.kmask);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (N * H * Sq == 0 || Sk == 0) {
         // no query or no key: every gradient is an empty sum (fp16 tensors have an even element

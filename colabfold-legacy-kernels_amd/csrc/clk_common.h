@@ -83,24 +83,6 @@ __device__ __forceinline__ float sigmoid_fast(float g) {
     return __builtin_amdgcn_rcpf(1.0f + exp2_fast(-kLog2e * g));
 }
 
-// 16 bits, one per byte of m (16 mask bytes), set where the byte is nonzero and its index is
-// below `valid`.
-__device__ __forceinline__ uint32_t mask_bits16(uint4 m, int valid) {
-    const uint32_t w[4] = {m.x, m.y, m.z, m.w};
-    uint32_t bits = 0u;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        // high bit of each byte set where that byte is nonzero
-        const uint32_t hi = ((w[q] & 0x7f7f7f7fu) + 0x7f7f7f7fu | w[q]) & 0x80808080u;
-        bits |= ((hi >> 7) & 1u) << (4 * q);
-        bits |= ((hi >> 15) & 1u) << (4 * q + 1);
-        bits |= ((hi >> 23) & 1u) << (4 * q + 2);
-        bits |= ((hi >> 31) & 1u) << (4 * q + 3);
-    }
-    const uint32_t in = valid >= 16 ? 0xffffu : valid <= 0 ? 0u : (1u << valid) - 1u;
-    return bits & in;
-}
-
 // Bias values of 16 consecutive keys (lo = keys 0..7, hi = 8..15) with key kk replaced by
 // `masked` where its keep bit is clear but it lies inside Sk, and by `outside` past Sk.
 __device__ __forceinline__ void fill_bias16(half8& lo, half8& hi, uint32_t keep, uint32_t inside,
