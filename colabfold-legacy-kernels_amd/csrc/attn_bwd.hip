@@ -242,54 +242,57 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
         // every key of the tile kept and inside Sk: the bias stands as loaded
         if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
 
-        float4v s[4][T::kQB], dp[4][T::kQB];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const int krw = 16 * kb + r16;  // key 16 (r/4) + 4 kb + r%4
-#pragma unroll
-            for (int qb = 0; qb < T::kQB; ++qb) {
-                s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
-                dp[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int ks = 0; ks < T::kKS; ++ks) {
-                const half8 kop = bld8(&Ks[krw * T::kLd + 32 * ks + 8 * g]);
-                const half8 vop = bld8(&Vs[krw * T::kLd + 32 * ks + 8 * g]);
-#pragma unroll
-                for (int qb = 0; qb < T::kQB; ++qb) {
-                    s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
-                    dp[kb][qb] = mfma16x16x32(vop, dop[qb][ks], dp[kb][qb]);
-                }
-            }
-        }
-
-        // dS^T = P^T (dP^T - delta), packed as the B operand of dQ^T; a dead logit has p = 0
-        half8 dsb[2][T::kQB];
-#pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) {
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int kk = 4 * kb + i;
-                    const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
-                    const float t = fmaf(s[kb][qb][i], scale, (float)b);
-                    const float p = exp2_fast(fmaf(t, kLog2e, -lse2[qb]));
-                    const float ds = p * (dp[kb][qb][i] - dlt[qb]);
-                    dsb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)pin_f32(ds);
-                }
-            }
-        }
-
+        // the tile in two halves of 32 keys: key blocks 2 kt and 2 kt + 1 hold keys 16 g + 8 kt + j,
+        // which are the k-slots of dQ^T's contraction step kt, so each half's S^T and dP^T
+        // registers are free again once its dS^T is packed
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
+            float4v s[2][T::kQB], dp[2][T::kQB];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const int krw = 16 * (2 * kt + k2) + r16;  // key 16 (r/4) + 4 kb + r%4
+#pragma unroll
+                for (int qb = 0; qb < T::kQB; ++qb) {
+                    s[k2][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                    dp[k2][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int ks = 0; ks < T::kKS; ++ks) {
+                    const half8 kop = bld8(&Ks[krw * T::kLd + 32 * ks + 8 * g]);
+                    const half8 vop = bld8(&Vs[krw * T::kLd + 32 * ks + 8 * g]);
+#pragma unroll
+                    for (int qb = 0; qb < T::kQB; ++qb) {
+                        s[k2][qb] = mfma16x16x32(kop, qop[qb][ks], s[k2][qb]);
+                        dp[k2][qb] = mfma16x16x32(vop, dop[qb][ks], dp[k2][qb]);
+                    }
+                }
+            }
+
+            // dS^T = P^T (dP^T - delta), packed as the B operand of dQ^T; a dead logit has p = 0
+            half8 dsb[T::kQB];
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) {
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = 4 * (2 * kt + k2) + i;
+                        const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
+                        const float t = fmaf(s[k2][qb][i], scale, (float)b);
+                        const float p = exp2_fast(fmaf(t, kLog2e, -lse2[qb]));
+                        const float ds = p * (dp[k2][qb][i] - dlt[qb]);
+                        dsb[qb][4 * k2 + i] = (half_t)pin_f32(ds);
+                    }
+                }
+            }
+
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
                 // K^T read transposed from the row-major K tile: slots are keys 16 g + 8 kt + j
                 const half8 kto = lds_operand_tr([&](int r) { return Ks + perm_row(r, 16) * T::kLd; },
                                                  2 * g + kt, r16, 4 * db, DP / 4);
 #pragma unroll
-                for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[kt][qb], acc[db][qb]);
+                for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[qb], acc[db][qb]);
             }
         }
         // the other buffer was last read a tile ago, before the barrier that ended that tile
