@@ -230,6 +230,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
         }
     };
 
+    // dP^T starts from -delta (the MFMA accumulator input), so dS = p dP is one multiply
+    float4v ndlt[T::kQB];
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) ndlt[qb] = float4v{-dlt[qb], -dlt[qb], -dlt[qb], -dlt[qb]};
+
     uint64_t keep_cur = 0u;
     const auto tile = [&](int k0, int buf, BH16 (&bias16)[T::kQB], BH16 (&bias_next)[T::kQB]) {
         const half_t* Ks = Ks2[buf];
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) {
                     s[k2][qb] = float4v{0.f, 0.f, 0.f, 0.f};
-                    dp[k2][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                    dp[k2][qb] = ndlt[qb];
                 }
 #pragma unroll
                 for (int ks = 0; ks < T::kKS; ++ks) {
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
                         const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
                         const float t = fmaf(s[k2][qb][i], scale, (float)b);
                         const float p = exp2_fast(fmaf(t, kLog2e, -lse2[qb]));
-                        const float ds = p * (dp[k2][qb][i] - dlt[qb]);
+                        const float ds = p * dp[k2][qb][i];
                         dsb[qb][4 * k2 + i] = (half_t)pin_f32(ds);
                     }
                 }
