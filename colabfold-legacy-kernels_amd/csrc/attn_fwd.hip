@@ -14,6 +14,8 @@
 // lane l holds keys 16 (l/16) + 4 kb + i of query l % 16, so the softmax statistics and the
 // O rescale are per-lane scalars, P^T feeds the second MFMA as its B operand without leaving
 // registers, and a lane's bias and mask are 16 contiguous elements of one row.
+#include <type_traits>
+
 #include "clk_common.h"
 
 namespace clk {
@@ -32,7 +34,7 @@ struct FwdArgs {
     int64_t qn, qh, qs, kn, kh, ks, on, oh, os;  // element strides of q/gate, k/v, out
     int N, H, Sq, Sk, D;
     float scale;
-    int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0)
+    int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0), one head's bias < 2^31 bytes
     int head_major;  // work items head-major ([N,H,S,D] tensors), else row-major (packed rows)
 };
 
@@ -81,7 +83,7 @@ __device__ __forceinline__ H16 load_h16(const half_t* p, int valid, bool vec) {
 }
 
 template <int DP, bool LSE, bool GATE, bool TRIM>
-__global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_fwd_kernel(FwdArgs a) {
     using T = FwdTile<DP>;
     // two key tiles in flight: one being read by the MFMAs, the next being written
     __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kKsLd];
@@ -203,6 +205,22 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         const int gqc = gq < a.Sq ? gq : a.Sq - 1;
         brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
     }
+    // where bias rows are whole 16-byte vectors (and a head's bias spans under 2^31 bytes): buffer
+    // loads whose range is the head's bias block, from a fixed lane offset. Keys past Sk read the
+    // next row's values or zeros; they become -inf when their tile comes up.
+    const half_t* const bias_head = a.bias + (int64_t)h * a.Sq * a.Sk;
+    uint32_t boff[T::kQB];
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) boff[qb] = (uint32_t)((brow[qb] - bias_head) * 2);
+    const auto fetch_bias_vec = [&](int k0, H16 (&b)[T::kQB]) {
+        const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(bias_head + k0), 0,
+                                                          (a.Sq * a.Sk - k0) * 2, 0x00020000);
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            b[qb].lo = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[qb], 0, 0));
+            b[qb].hi = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[qb] + 16, 0, 0));
+        }
+    };
     const auto fetch_bias = [&](int k0, H16 (&b)[T::kQB]) {
         if (a.bias_vec && k0 + T::kBK <= a.Sk) {
 #pragma unroll
@@ -226,15 +244,27 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
         }
     };
 
-    // one key tile: prefetch the next, then S^T, the online softmax and O^T += V^T P^T
+    // One key tile: prefetch the next, then S^T, the online softmax and O^T += V^T P^T. On the
+    // vector path every prefetch load is issued unconditionally (the last tile loads and stages
+    // itself again into the idle buffer), so the tile is straight-line code and each wait
+    // covers only the loads it needs.
     uint64_t keep_cur = 0u;
-    const auto tile = [&](int k0, int buf, H16 (&bias16)[T::kQB], H16 (&bias_next)[T::kQB]) {
+    const int k_last = (k_end - 1) / T::kBK * T::kBK;
+    const auto tile = [&](auto vec, int k0, int buf, H16 (&bias16)[T::kQB],
+                          H16 (&bias_next)[T::kQB]) __attribute__((always_inline)) {
         const half_t* Ks = Ks2[buf];
         const half_t* Vs = Vs2[buf];
-        const bool more = k0 + T::kBK < k_end;
-        if (more) {
-            fetch(k0 + T::kBK);
-            fetch_bias(k0 + T::kBK, bias_next);
+        bool more = true;
+        if constexpr (decltype(vec)::value) {
+            const int kn = min(k0 + T::kBK, k_last);
+            fetch(kn);
+            fetch_bias_vec(kn, bias_next);
+        } else {
+            more = k0 + T::kBK < k_end;
+            if (more) {
+                fetch(k0 + T::kBK);
+                fetch_bias(k0 + T::kBK, bias_next);
+            }
         }
         // every key of the tile kept and inside Sk: the bias stands as loaded
         if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
@@ -331,16 +361,27 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads) void attn_fwd_kernel(FwdArgs
     };
 
     H16 biasA[T::kQB], biasB[T::kQB];
-    if (k_end > 0) {
+    const auto run = [&](auto vec) __attribute__((always_inline)) {
         fetch(0);
-        fetch_bias(0, biasA);
+        if constexpr (decltype(vec)::value) {
+            fetch_bias_vec(0, biasA);
+        } else {
+            fetch_bias(0, biasA);
+        }
         keep_cur = __ballot(mbyte != 0u);
         stage(0, keep_cur);
         __syncthreads();
-    }
-    for (int k0 = 0; k0 < k_end; k0 += 2 * T::kBK) {
-        tile(k0, 0, biasA, biasB);
-        if (k0 + T::kBK < k_end) tile(k0 + T::kBK, 1, biasB, biasA);
+        for (int k0 = 0; k0 < k_end; k0 += 2 * T::kBK) {
+            tile(vec, k0, 0, biasA, biasB);
+            if (k0 + T::kBK < k_end) tile(vec, k0 + T::kBK, 1, biasB, biasA);
+        }
+    };
+    if (k_end > 0) {
+        if (a.bias_vec) {
+            run(std::true_type{});
+        } else {
+            run(std::false_type{});
+        }
     }
 
     // epilogue: lane g holds d = (DP/4) g .. +DP/4 of query q0w + 16 qb + r16
@@ -476,7 +517,7 @@ extern "C" int clk_attention_fwd(clk_stream stream, int32_t device, const clk_bu
     a.out = static_cast<half_t*>(out->data);
     a.lse = want_lse ? static_cast<float*>(lse->data) : nullptr;
     a.scale = scale;
-    a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
+    a.bias_vec = Sk % 8 == 0 && aligned16(a.bias) && (int64_t)Sq * Sk * 2 < ((int64_t)1 << 31);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     return want_lse ? dispatch_fwd<true, false, false>(s, device, a)
                     : dispatch_fwd<false, false, false>(s, device, a);
@@ -530,7 +571,7 @@ static int packed_common(clk_stream stream, int32_t device, const clk_buffer* p,
     a.out = static_cast<half_t*>(out->data);
     a.lse = nullptr;
     a.scale = scale;
-    a.bias_vec = S % 8 == 0 && aligned16(a.bias);
+    a.bias_vec = S % 8 == 0 && aligned16(a.bias) && (int64_t)S * S * 2 < ((int64_t)1 << 31);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (lims) {
         return G == 4 ? dispatch_fwd<false, true, true>(s, device, a)
