@@ -53,6 +53,7 @@ struct BwdArgs {
     float c1s;   // c1 / log2e: scale, or the stand-in's 1 / log2e
     int kscale;  // 0 where c1 stands in for a negligible scale: the dK/dV kernel's K is then zero
     int bias_vec;
+    int dbias_vec;  // dbias rows are whole 16-byte vectors (Sk % 4 == 0, 16-byte aligned)
 };
 
 __device__ __forceinline__ half8 bzero8() {
@@ -742,42 +743,45 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
     }
 }
 
-// dbias[h][q][64 kblk + kk] = sum over chunks, in chunk order, of partial[c][h][kblk][q][kk]: a
-// workgroup covers 64 query rows of one key block; a thread four keys (one 16-byte load) of four
-// rows 16 apart
+// dbias[h][q][key] = the chunks' partials summed in chunk order. A workgroup takes 16 queries x
+// 64 keys of one head, a thread four keys of one query; its chunk loads are issued eight at a
+// time ahead of their adds, so many are in flight per thread.
 __global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(BwdArgs a) {
-    const int qgroups = (a.SqA + 63) / 64;
+    const int qgroups = a.SqA / 16;
     const int item = blockIdx.x;
     const int qgrp = item % qgroups, rest = item / qgroups;
     const int kblk = rest % a.kblocks, h = rest / a.kblocks;
-    const int k4 = (threadIdx.x & 15) * 4, q0 = qgrp * 64 + (threadIdx.x >> 4);
+    const int k4 = (threadIdx.x & 15) * 4, q = qgrp * 16 + (threadIdx.x >> 4);
     const int64_t stride = (int64_t)a.H * a.kblocks * a.SqA * 64;
-    const float* src = a.partial + ((int64_t)h * a.kblocks + kblk) * a.SqA * 64 + k4;
-    float4 sum[4];
+    const float* src = a.partial + (((int64_t)h * a.kblocks + kblk) * a.SqA + q) * 64 + k4;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    int c = 0;
+    for (; c + 8 <= a.chunks; c += 8) {
+        float4 v[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sum[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    // the adds stay in chunk order; unrolling only puts more loads in flight
-#pragma unroll 4
-    for (int c = 0; c < a.chunks; ++c) {
+        for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const float4*>(src + (c + j) * stride);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int q = q0 + 16 * r;
-            if (q < a.SqA) {
-                const float4 v = *reinterpret_cast<const float4*>(src + c * stride + (int64_t)q * 64);
-                sum[r].x += v.x;
-                sum[r].y += v.y;
-                sum[r].z += v.z;
-                sum[r].w += v.w;
-            }
+        for (int j = 0; j < 8; ++j) {
+            sum.x += v[j].x;
+            sum.y += v[j].y;
+            sum.z += v[j].z;
+            sum.w += v[j].w;
         }
     }
+    for (; c < a.chunks; ++c) {
+        const float4 v = *reinterpret_cast<const float4*>(src + c * stride);
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+    }
+    if (q >= a.Sq) return;
     const int key = kblk * 64 + k4;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int q = q0 + 16 * r;
-        if (q >= a.Sq) continue;
-        float* dst = a.dbias + ((int64_t)h * a.Sq + q) * a.Sk + key;
-        const float v[4] = {sum[r].x, sum[r].y, sum[r].z, sum[r].w};
+    float* dst = a.dbias + ((int64_t)h * a.Sq + q) * a.Sk + key;
+    if (a.dbias_vec && key + 4 <= a.Sk) {
+        *reinterpret_cast<float4*>(dst) = sum;
+    } else {
+        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if (key + j < a.Sk) dst[j] = v[j];
@@ -929,7 +933,7 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     }
     stage_mark(stream, 3);
     if (want_dbias) {
-        const int64_t g3 = (int64_t)((a.SqA + 63) / 64) * p.kblocks * a.H;
+        const int64_t g3 = (int64_t)(a.SqA / 16) * p.kblocks * a.H;
         hipLaunchKernelGGL(attn_bwd_dbias_kernel, dim3((unsigned)g3), dim3(256), 0, stream, a);
     } else {
         const int64_t nb = (int64_t)a.H * a.Sq * a.Sk;
@@ -1025,6 +1029,7 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     if (!a.kscale) a.c1 = 1.f;  // scale log2e S is below fp32 resolution against the bias
     a.c1s = a.c1 / kLog2e;
     a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
+    a.dbias_vec = Sk % 4 == 0 && aligned16(a.dbias);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (N * H * Sq == 0 || Sk == 0) {
         // no query or no key: every gradient is an empty sum (fp16 tensors have an even element
