@@ -477,29 +477,27 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         reinterpret_cast<const char*>(a.biast + ((int64_t)h * a.SkA + kblk * T::kBK) * a.SqA);
     const uint32_t bt_off = (uint32_t)(klocal * a.SqA + 8 * g) * 2u;
 
-    // A step's Q / dO chunks and query terms: two register sets, one per step parity, fetched
-    // two steps ahead of their stage. The bias: two register sets likewise, two steps ahead of
+    // A step's Q / dO chunks: two register sets, one per step parity, fetched two steps ahead of
+    // their stage. The bias and the query term: two register sets likewise, two steps ahead of
     // their use. (Padded past Sq: -lse2 / c1 infinite, -delta 0, bias 0.)
     struct Chunks {
         half8 s[T::kCPT];
-        float st;
     };
     Chunks ch0, ch1;
-    float stc = 0.f;  // the staged step's query term
     half8 bt0, bt1;
+    float sq0, sq1;
     // The chunk and bias prefetches walk the steps with cursors of their own, ahead of the
     // step being computed; a cursor past the last pass reads zeros (chunks) or a valid tile
     // (bias), unused.
     int cs_pass = 0, cs_it = 0, cs_tile = tile_of(0);
     bool cs_rowv = false;
-    const char *cs_q = nullptr, *cs_o = nullptr, *cs_st = nullptr;
+    const char *cs_q = nullptr, *cs_o = nullptr;
     const auto cs_row = [&]() {
         const int n = n_begin + rg + QG * cs_pass;
         cs_rowv = n < n_end;
         const int64_t nh = (int64_t)(cs_rowv ? n : n_begin) * a.H + h;
         cs_q = reinterpret_cast<const char*>(a.q + nh * a.Sq * a.D);
         cs_o = reinterpret_cast<const char*>(a.dout + nh * a.Sq * a.D);
-        cs_st = reinterpret_cast<const char*>(a.qstat + nh * a.SqA * 2);
     };
     const auto fetch_s = [&](Chunks& d) {
         const int q0 = cs_tile * T::kBQ;
@@ -511,7 +509,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(src), 0, bytes, 0x00020000);
             d.s[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff[i], 0, 0));
         }
-        d.st = *reinterpret_cast<const float*>(cs_st + q0 * 8 + st_off);
         if (++cs_it == qsteps) {
             cs_it = 0;
             ++cs_pass;
@@ -519,10 +516,22 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         }
         cs_tile = tile_of(cs_it);
     };
-    int bc_it = 0;
-    const auto fetch_c = [&](half8& d) {
-        d = *reinterpret_cast<const half8*>(bt_base + tile_of(bc_it) * (T::kBQ * 2) + bt_off);
-        if (++bc_it == qsteps) bc_it = 0;
+    int bc_pass = 0, bc_it = 0;
+    const char* bc_st = nullptr;
+    const auto bc_row = [&]() {
+        const int n = n_begin + rg + QG * bc_pass;
+        const int64_t nh = (int64_t)(n < n_end ? n : n_begin) * a.H + h;
+        bc_st = reinterpret_cast<const char*>(a.qstat + nh * a.SqA * 2);
+    };
+    const auto fetch_c = [&](half8& d, float& sq) {
+        const int q0 = tile_of(bc_it) * T::kBQ;
+        d = *reinterpret_cast<const half8*>(bt_base + q0 * 2 + bt_off);
+        sq = *reinterpret_cast<const float*>(bc_st + q0 * 8 + st_off);
+        if (++bc_it == qsteps) {
+            bc_it = 0;
+            ++bc_pass;
+            bc_row();
+        }
     };
     const auto stage_tile = [&](const Chunks& d, int buf) {
         half_t* Qs = stage0 + buf * kBufStride;
@@ -531,7 +540,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
             *reinterpret_cast<half4*>(Qs + cdst0[i]) = half4{d.s[i][0], d.s[i][1], d.s[i][2], d.s[i][3]};
             *reinterpret_cast<half4*>(Qs + cdst1[i]) = half4{d.s[i][4], d.s[i][5], d.s[i][6], d.s[i][7]};
         }
-        stc = d.st;
     };
 
     // K and V of this group's next row as the B operands (lane column = key, slots
@@ -558,12 +566,13 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     float4v accv[T::kDB], acck[T::kDB];
 
     cs_row();
+    bc_row();
     if (rows > 0) {
         fetch_kv(0);
         fetch_s(ch0);
         fetch_s(ch1);
-        fetch_c(bt0);
-        fetch_c(bt1);
+        fetch_c(bt0, sq0);
+        fetch_c(bt1, sq1);
         stage_tile(ch0, 0);
         fetch_s(ch0);
     }
@@ -573,7 +582,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     // with the step two on once consumed; at its end it stages the next step from the chunk set
     // of that parity and refills the set with the step three on (steps past the end load the
     // last step again, unused)
-    const auto step = [&](int it, Chunks& next, half8& bt) {
+    const auto step = [&](int it, Chunks& next, half8& bt, float& sq) {
         const int buf = it & 1, q0 = tile_of(it) * T::kBQ;
         const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
@@ -587,8 +596,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 const int qrow = 16 * qb + r16;
-                float4v s = qb == 0 ? row_quad<0>(stc) : row_quad<4>(stc);
-                dp[qb] = qb == 0 ? row_quad<8>(stc) : row_quad<12>(stc);
+                float4v s = qb == 0 ? row_quad<0>(sq) : row_quad<4>(sq);
+                dp[qb] = qb == 0 ? row_quad<8>(sq) : row_quad<12>(sq);
 #pragma unroll
                 for (int ks = 0; ks < T::kKS; ++ks) {
                     const int w0 = 2 * dkdv_word(qrow, 32 * ks + 8 * g);
@@ -650,7 +659,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 acck[db] = mfma16x16x32(qt, dsb, acck[db]);
             }
         }
-        fetch_c(bt);  // the bias two steps on, into the registers just consumed
+        fetch_c(bt, sq);  // the bias and query term two steps on, into the registers just consumed
         // the other buffer was last read a step ago, before the barrier that ended that step
         stage_tile(next, buf ^ 1);
         fetch_s(next);  // the chunks three steps on
@@ -675,8 +684,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         fetch_kv(pass + 1 < rows ? pass + 1 : pass);
 
         for (int it = 0; it < qsteps; it += 2) {
-            step(it, ch1, bt0);
-            step(it + 1, ch0, bt1);
+            step(it, ch1, bt0, sq0);
+            step(it + 1, ch0, bt1, sq1);
         }
 
         if (nv && kin) {
