@@ -591,6 +591,15 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
         // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
         if (valid) {
+            // this lane's dBias partial elements, read ahead of the S and dP products (the row
+            // groups' tiles are disjoint at every step, and this lane is the only writer of these
+            // eight elements within its group; LDS float atomics measured several times slower)
+            float* dbrow = DBt + (q0 / 4 + 2 * g) * (4 * T::kBK) + 4 * klocal;
+            float4 dblo, dbhi;
+            if constexpr (DBIAS) {
+                dblo = *reinterpret_cast<float4*>(dbrow);
+                dbhi = *reinterpret_cast<float4*>(dbrow + 4 * T::kBK);
+            }
             float x[8];
             float4v dp[2];
 #pragma unroll
@@ -637,16 +646,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) dsb[j] = (half_t)dsf[j];
             if constexpr (DBIAS) {
-                // the row groups' tiles are disjoint at every step, and this lane is the only
-                // writer of these eight elements within its group (a read-modify-write: LDS float
-                // atomics measured several times slower here)
-                float* row = DBt + (q0 / 4 + 2 * g) * (4 * T::kBK) + 4 * klocal;
-                float4 lo = *reinterpret_cast<float4*>(row);
-                float4 hi = *reinterpret_cast<float4*>(row + 4 * T::kBK);
-                lo.x += dsf[0]; lo.y += dsf[1]; lo.z += dsf[2]; lo.w += dsf[3];
-                hi.x += dsf[4]; hi.y += dsf[5]; hi.z += dsf[6]; hi.w += dsf[7];
-                *reinterpret_cast<float4*>(row) = lo;
-                *reinterpret_cast<float4*>(row + 4 * T::kBK) = hi;
+                dblo.x += dsf[0]; dblo.y += dsf[1]; dblo.z += dsf[2]; dblo.w += dsf[3];
+                dbhi.x += dsf[4]; dbhi.y += dsf[5]; dbhi.z += dsf[6]; dbhi.w += dsf[7];
+                *reinterpret_cast<float4*>(dbrow) = dblo;
+                *reinterpret_cast<float4*>(dbrow + 4 * T::kBK) = dbhi;
             }
 
             // dV^T += dO^T P, dK^T += Q^T dS: A row r of d block db is
