@@ -135,11 +135,14 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         }
     }
 
-    float m_run[T::kQB], l_run[T::kQB];
+    // running max m, its exp2-domain negative -m log2e and raise threshold m log2e + 6, and l
+    float m_run[T::kQB], nm2[T::kQB], thr[T::kQB], l_run[T::kQB];
     float4v acc[T::kDB][T::kQB];
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) {
         m_run[qb] = -INFINITY;
+        nm2[qb] = 0.f;
+        thr[qb] = -INFINITY;
         l_run[qb] = 0.f;
 #pragma unroll
         for (int db = 0; db < T::kDB; ++db) acc[db][qb] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -308,35 +311,36 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         // the same; the cross-lane maximum is only needed on a tile that raises.
         bool up = false;
 #pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) up |= m_tile[qb] * kLog2e > m_run[qb] * kLog2e + 6.f;
-        const bool raise = __any(up);
-        if (raise) {
+        for (int qb = 0; qb < T::kQB; ++qb) up |= m_tile[qb] * kLog2e > thr[qb];
+        if (__any(up)) {
+            // the running max moves (always on the first tile): rescale l and O by 2^(m - m_new)
 #pragma unroll
-            for (int qb = 0; qb < T::kQB; ++qb) m_tile[qb] = wave_xor_max4(m_tile[qb]);
+            for (int qb = 0; qb < T::kQB; ++qb) {
+                const float m_new = fmaxf(m_run[qb], wave_xor_max4(m_tile[qb]));
+                const float alpha = exp2_fast((m_run[qb] - m_new) * kLog2e);
+                l_run[qb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < T::kDB; ++db) acc[db][qb] *= alpha;
+                m_run[qb] = m_new;
+                nm2[qb] = -m_new * kLog2e;
+                thr[qb] = m_new * kLog2e + 6.f;
+            }
         }
 
         half8 pb[2][T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
-            const float m_new = raise ? fmaxf(m_run[qb], m_tile[qb]) : m_run[qb];
-            const float alpha = raise ? exp2_fast((m_run[qb] - m_new) * kLog2e) : 1.f;
-            const float nm2 = -m_new * kLog2e;
             float lsum = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float p = exp2_fast(fmaf(s[kb][qb][i], kLog2e, nm2));
+                    const float p = exp2_fast(fmaf(s[kb][qb][i], kLog2e, nm2[qb]));
                     lsum += p;
                     pb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)p;
                 }
             }
-            l_run[qb] = l_run[qb] * alpha + lsum;
-            m_run[qb] = m_new;
-            if (raise) {
-#pragma unroll
-                for (int db = 0; db < T::kDB; ++db) acc[db][qb] *= alpha;
-            }
+            l_run[qb] += lsum;
         }
 
         // O^T += V^T P^T: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4; slot 8 g + j of
