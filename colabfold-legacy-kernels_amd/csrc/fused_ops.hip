@@ -42,6 +42,12 @@ __device__ __forceinline__ half8 fzero8() {
 }
 __device__ __forceinline__ half8 fld8(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
 __device__ __forceinline__ void fst8(half_t* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
+// A streaming (nontemporal) 16-byte store, for outputs that no later kernel of the op reads back
+// soon; measured faster for the wide outputs of ln_projection at c = 128 and ln_gdp, slower for
+// ln_projection at c = 64, where two workgroups share a CU.
+__device__ __forceinline__ void fst8_nt(half_t* p, half8 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<half8*>(p));
+}
 
 // operand chunk (block, step, lane) of a fragment-major matrix with KS contraction steps
 __device__ __forceinline__ int frag(int block, int ks, int KS, int lane) {
@@ -450,7 +456,11 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
 #pragma unroll
                     for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[pp][j]);
                 }
-                fst8(a.out + (int64_t)row * a.n + col, o);
+                if constexpr (K == 128) {
+                    fst8_nt(a.out + (int64_t)row * a.n + col, o);
+                } else {
+                    fst8(a.out + (int64_t)row * a.n + col, o);
+                }
             }
         }
         if (heads_wave) {
@@ -590,8 +600,8 @@ __global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
                 }
             const int rows_left = a.M - (m0 + 16 * g);
             if (vec && rows_left >= 16) {
-                fst8(dst, lo);
-                fst8(dst + 8, hi);
+                fst8_nt(dst, lo);
+                fst8_nt(dst + 8, hi);
             } else {
 #pragma unroll
                 for (int t = 0; t < 16; ++t)
