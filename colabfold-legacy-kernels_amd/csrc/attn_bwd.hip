@@ -579,72 +579,82 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     __syncthreads();
 
     // step (pass, it) reads LDS buffer it & 1 and the bias set of its parity, which it refills
-    // with the step two on once consumed; at its end it stages the next step from the chunk set
-    // of that parity and refills the set with the step three on (steps past the end load the
-    // last step again, unused)
+    // with the step two on once consumed; after its S and dP products it stages the next step
+    // from the chunk set of that parity and refills the set with the step three on (steps past
+    // the end load the last step again, unused)
     const auto step = [&](int it, Chunks& next, half8& bt, float& sq) {
         const int buf = it & 1, q0 = tile_of(it) * T::kBQ;
         const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
         const half_t* Os = Qs + T::kOs;
 
+        // The S and dP products, the exp and dS run on every step (an idle step reads zeros
+        // from its staged tile and finite query terms, and its results are dropped), so the
+        // step's prefetch and staging sit in straight-line code between them; only the
+        // accumulations are skipped on an idle step.
+        // This lane's dBias partial elements are read first, ahead of the S and dP products (the
+        // row groups' tiles are disjoint at every step, also on idle steps, and this lane is the
+        // only writer of these eight elements within its group; LDS float atomics measured
+        // several times slower).
+        float* dbrow = DBt + (q0 / 4 + 2 * g) * (4 * T::kBK) + 4 * klocal;
+        float4 dblo, dbhi;
+        if constexpr (DBIAS) {
+            dblo = *reinterpret_cast<float4*>(dbrow);
+            dbhi = *reinterpret_cast<float4*>(dbrow + 4 * T::kBK);
+        }
         // S (from -lse2 / c1) and dP (from -delta): A row r of query block qb is query
         // 8 (r/4) + 4 qb + r%4 of the tile, so the lane holds queries 8 g + 4 qb + i
-        if (valid) {
-            // this lane's dBias partial elements, read ahead of the S and dP products (the row
-            // groups' tiles are disjoint at every step, and this lane is the only writer of these
-            // eight elements within its group; LDS float atomics measured several times slower)
-            float* dbrow = DBt + (q0 / 4 + 2 * g) * (4 * T::kBK) + 4 * klocal;
-            float4 dblo, dbhi;
-            if constexpr (DBIAS) {
-                dblo = *reinterpret_cast<float4*>(dbrow);
-                dbhi = *reinterpret_cast<float4*>(dbrow + 4 * T::kBK);
+        float x[8];
+        float4v dp[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qrow = 16 * qb + r16;
+            float4v s = qb == 0 ? row_quad<0>(sq) : row_quad<4>(sq);
+            dp[qb] = qb == 0 ? row_quad<8>(sq) : row_quad<12>(sq);
+#pragma unroll
+            for (int ks = 0; ks < T::kKS; ++ks) {
+                const int w0 = 2 * dkdv_word(qrow, 32 * ks + 8 * g);
+                const int w1 = 2 * dkdv_word(qrow, 32 * ks + 8 * g + 4);
+                const half4 q0v = *reinterpret_cast<const half4*>(Qs + w0);
+                const half4 q1v = *reinterpret_cast<const half4*>(Qs + w1);
+                const half4 o0v = *reinterpret_cast<const half4*>(Os + w0);
+                const half4 o1v = *reinterpret_cast<const half4*>(Os + w1);
+                const half8 qa = half8{q0v[0], q0v[1], q0v[2], q0v[3], q1v[0], q1v[1], q1v[2], q1v[3]};
+                const half8 oa = half8{o0v[0], o0v[1], o0v[2], o0v[3], o1v[0], o1v[1], o1v[2], o1v[3]};
+                s = mfma16x16x32(qa, kop[ks], s);
+                dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
             }
-            float x[8];
-            float4v dp[2];
+            // s2 = log2e (scale S + bias); a dead key (K zero) takes the masked logit
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                const int qrow = 16 * qb + r16;
-                float4v s = qb == 0 ? row_quad<0>(sq) : row_quad<4>(sq);
-                dp[qb] = qb == 0 ? row_quad<8>(sq) : row_quad<12>(sq);
-#pragma unroll
-                for (int ks = 0; ks < T::kKS; ++ks) {
-                    const int w0 = 2 * dkdv_word(qrow, 32 * ks + 8 * g);
-                    const int w1 = 2 * dkdv_word(qrow, 32 * ks + 8 * g + 4);
-                    const half4 q0v = *reinterpret_cast<const half4*>(Qs + w0);
-                    const half4 q1v = *reinterpret_cast<const half4*>(Qs + w1);
-                    const half4 o0v = *reinterpret_cast<const half4*>(Os + w0);
-                    const half4 o1v = *reinterpret_cast<const half4*>(Os + w1);
-                    const half8 qa = half8{q0v[0], q0v[1], q0v[2], q0v[3], q1v[0], q1v[1], q1v[2], q1v[3]};
-                    const half8 oa = half8{o0v[0], o0v[1], o0v[2], o0v[3], o1v[0], o1v[1], o1v[2], o1v[3]};
-                    s = mfma16x16x32(qa, kop[ks], s);
-                    dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
-                }
-                // s2 = log2e (scale S + bias); a dead key (K zero) takes the masked logit
-#pragma unroll
-                for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1s, (float)bt[4 * qb + i]) * kLog2e;
-                if (!all_alive) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        x[4 * qb + i] = alive ? x[4 * qb + i] : fmaf(s[i], c1s, kMaskedLogit) * kLog2e;
-                    }
-                }
-            }
-            half8 pb, dsb;
-            float dsf[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = exp2_fast(x[j]);
-                dsf[j] = pin_f32(p * dp[j >> 2][j & 3]);
-                pb[j] = (half_t)p;
-            }
+            for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1s, (float)bt[4 * qb + i]) * kLog2e;
             if (!all_alive) {
-                // a dead key's dS is 0 (its p, from the masked logit, still carries dV)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) dsf[j] = alive ? dsf[j] : 0.f;
+                for (int i = 0; i < 4; ++i) {
+                    x[4 * qb + i] = alive ? x[4 * qb + i] : fmaf(s[i], c1s, kMaskedLogit) * kLog2e;
+                }
             }
+        }
+        fetch_c(bt, sq);  // the bias and query term two steps on, into the registers just consumed
+        // the other buffer was last read a step ago, before the barrier that ended that step
+        stage_tile(next, buf ^ 1);
+        fetch_s(next);  // the chunks three steps on
+
+        half8 pb, dsb;
+        float dsf[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) dsb[j] = (half_t)dsf[j];
+        for (int j = 0; j < 8; ++j) {
+            const float p = exp2_fast(x[j]);
+            dsf[j] = pin_f32(p * dp[j >> 2][j & 3]);
+            pb[j] = (half_t)p;
+        }
+        if (!all_alive) {
+            // a dead key's dS is 0 (its p, from the masked logit, still carries dV)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dsf[j] = alive ? dsf[j] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dsb[j] = (half_t)dsf[j];
+        if (valid) {
             if constexpr (DBIAS) {
                 dblo.x += dsf[0]; dblo.y += dsf[1]; dblo.z += dsf[2]; dblo.w += dsf[3];
                 dbhi.x += dsf[4]; dbhi.y += dsf[5]; dbhi.z += dsf[6]; dbhi.w += dsf[7];
@@ -662,10 +672,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 acck[db] = mfma16x16x32(qt, dsb, acck[db]);
             }
         }
-        fetch_c(bt, sq);  // the bias and query term two steps on, into the registers just consumed
-        // the other buffer was last read a step ago, before the barrier that ended that step
-        stage_tile(next, buf ^ 1);
-        fetch_s(next);  // the chunks three steps on
         __syncthreads();
     };
 
