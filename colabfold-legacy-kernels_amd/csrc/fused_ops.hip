@@ -611,6 +611,153 @@ __global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
     }
 }
 
+// The same op for M % 8 == 0 (16-byte channel-major stores), with a tile body that is straight-line
+// code, so that no wait for a load also waits for the stores issued before it (vmcnt counts
+// loads and stores in issue order, and the compiler's count is only as good as its weakest path):
+// - the next tile's mask rows are fetched with its x rows, and the keep decision is taken from
+//   them in registers (every wave's four lane groups hold all 64 rows, so a wave-wide any gives
+//   the workgroup's decision without LDS or a barrier);
+// - the loop is rotated so that the next tile's rows are fetched, the current tile's results
+//   stored, and then the fetched rows waited for (keep decision, LayerNorm) in the same iteration;
+// - every tile runs the LayerNorm and the GEMMs; a padding tile stores zeros, and the stores of a
+//   skipped tile and of rows past M are buffer stores at an offset past the buffer's end, which
+//   the hardware drops, so every tile issues the same stores and no branch skips them;
+// - each wave owns CBW column blocks, fixed at compile time, with their biases in registers.
+// Offsets are 32-bit: the launcher requires P/2 * M * 2 bytes < 2^31.
+template <int K, int PH, int TH>
+__global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
+    constexpr int KS = K / 32, TW = TH / kWave, NB = PH / 8, CBW = NB / TW;
+    static_assert(NB % TW == 0, "whole column blocks per wave");
+    constexpr uint32_t kDrop = 0x80000000u;  // a store offset past every buffer's end
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    half_t* Wp = lds;
+    half_t* Wg = Wp + 2 * PH * K;
+    half_t* Xf = Wg + 2 * PH * K;
+    float* sc = reinterpret_cast<float*>(Xf + kTileRows * K);
+    float* of = sc + K;
+    load_weight_frags<K, false>(Wp, a.wpT, 2 * PH, NB);
+    load_weight_frags<K, false>(Wg, a.wgT, 2 * PH, NB);
+    for (int i = threadIdx.x; i < K; i += TH) {
+        sc[i] = a.scale[i];
+        of[i] = a.offset[i];
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: scalar descriptors
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int G = gridDim.x;
+    const uint32_t out_bytes = (uint32_t)PH * (uint32_t)a.M * 2u;
+    const auto rl = __builtin_amdgcn_make_buffer_rsrc(a.left, 0, out_bytes, 0x00020000);
+    const auto rr = __builtin_amdgcn_make_buffer_rsrc(a.right, 0, out_bytes, 0x00020000);
+
+    float bpv[CBW], bgv[CBW];
+#pragma unroll
+    for (int j = 0; j < CBW; ++j) {
+        const int col = 16 * (wave + j * TW) + r16;
+        bpv[j] = (float)a.bp[col];
+        bgv[j] = (float)a.bg[col];
+    }
+
+    // rows of tile t (rows past M repeat row M - 1) and the mask of lane group g's 16 rows (the
+    // 8-row chunks are all in or all out since M % 8 == 0; those past M are replaced at use)
+    RowTile<K, kTileRows, TH> xt;
+    half8 mlo, mhi;
+    const auto fetch = [&](int t) {
+        const int r0 = t * kTileRows + 16 * g;
+        mlo = fld8(a.mask + min(r0, a.M - 8));
+        mhi = fld8(a.mask + min(r0 + 8, a.M - 8));
+        constexpr int TPR = RowTile<K, kTileRows, TH>::kTPR;
+        const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+        const int m = min(t * kTileRows + row, a.M - 1);
+#pragma unroll
+        for (int j = 0; j < RowTile<K, kTileRows, TH>::kChunks; ++j)
+            xt.v[j] = fld8(a.x + (int64_t)m * K + 8 * (part + TPR * j));
+    };
+    // the reference's keep rule for the tile (rows past M count as 0) and the rows' max(mask, 0)
+    float mv[16];
+    const auto decide = [&](int t) {
+        const int r0 = t * kTileRows + 16 * g;
+        bool live = false, zero = false;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float k = r0 + e < a.M ? (float)(e < 8 ? mlo[e] : mhi[e - 8]) : 0.f;
+            live |= k > 0.f;
+            zero |= k == 0.f;
+            mv[e] = fmaxf(k, 0.f);
+        }
+        const bool any_live = __any(live), any_zero = __any(zero);
+        return any_live ? (int)kCompute : any_zero ? (int)kPadding : (int)kSkip;
+    };
+    const auto gemm_store = [&](int t, int work) {
+        const int m0 = t * kTileRows;
+        half8 xop[4][KS];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(rb, ks, KS, lane));
+        const bool zero_out = work == kPadding;
+        const int rows_left = a.M - (m0 + 16 * g);  // <= 0, 8 or >= 16
+        const bool st_lo = work != kSkip && rows_left >= 8, st_hi = work != kSkip && rows_left >= 16;
+#pragma unroll
+        for (int j = 0; j < CBW; ++j) {
+            const int cb = wave + j * TW;
+            float4v ap[4], ag[4];
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                ap[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                ag[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 wp = fld8(Wp + frag(cb, ks, KS, lane));
+                const half8 wg = fld8(Wg + frag(cb, ks, KS, lane));
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    ap[rb] = mfma16x16x32(xop[rb][ks], wp, ap[rb]);
+                    ag[rb] = mfma16x16x32(xop[rb][ks], wg, ag[rb]);
+                }
+            }
+            half8 lo, hi;
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int e = 4 * rb + i;
+                    float v = mv[e] * (ap[rb][i] + bpv[j]) * sigmoid_fast(ag[rb][i] + bgv[j]);
+                    v = zero_out ? 0.f : v;
+                    if (e < 8) lo[e] = (half_t)v; else hi[e - 8] = (half_t)v;
+                }
+            // column block cb lies wholly in left (columns < PH) or in right
+            const int col = 16 * cb + r16;
+            const bool is_left = 16 * cb < PH;
+            const uint32_t off = ((uint32_t)(is_left ? col : col - PH) * (uint32_t)a.M + (uint32_t)(m0 + 16 * g)) * 2u;
+            const auto rs = is_left ? rl : rr;
+            // aux 2: nontemporal
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), rs, st_lo ? off : kDrop, 0, 2);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), rs, st_hi ? off + 16u : kDrop, 0, 2);
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= tiles) return;
+    fetch(t);
+    int work = decide(t);
+    ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
+    __syncthreads();
+    for (;;) {
+        const int nt = t + G;
+        fetch(min(nt, tiles - 1));
+        gemm_store(t, work);
+        if (nt >= tiles) break;
+        t = nt;
+        work = decide(t);
+        __syncthreads();  // every wave has read the previous tile's operands
+        ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
+        __syncthreads();
+    }
+}
+
 // ---- trimul_epilogue --------------------------------------------------------------------------
 
 struct EpiArgs {
@@ -1052,6 +1199,19 @@ extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buff
     const int64_t tiles = (M + kTileRows - 1) / kTileRows;
     const dim3 grid(persistent_grid(tiles, lds));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (M % 8 == 0 && P / 2 * M * 2 < (int64_t{1} << 31)) {  // 16-byte channel-major stores, 32-bit offsets
+#define CLK_GDP_FAST(K_, PH_)                                                                          \
+    if (K == K_ && P / 2 == PH_) {                                                                     \
+        const auto kern = ln_gdp_fast_kernel<K_, PH_, gdp_threads<K_>()>;                              \
+        if (int st = launch_fused("ln_gdp", kern, grid, lds, s, &a, 0)) return st;                     \
+        stage_mark(s, 0);                                                                              \
+        hipLaunchKernelGGL(kern, grid, dim3(gdp_threads<K_>()), lds, s, a);                            \
+        stage_mark(s, 1);                                                                              \
+        return launch_status("ln_gdp");                                                                \
+    }
+        CLK_GDP_FAST(64, 64) CLK_GDP_FAST(64, 128) CLK_GDP_FAST(128, 64) CLK_GDP_FAST(128, 128)
+#undef CLK_GDP_FAST
+    }
     if (K == 64) {
         if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64, gdp_threads<64>()>, grid, lds, s, &a, 0)) return st;
         stage_mark(s, 0);

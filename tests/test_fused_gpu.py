@@ -264,3 +264,53 @@ def test_keep_below_zero_writes_nothing(hip):
     wp, wb = orf.ln_projection(x, sc, of, wT, wbT, None, EPS)
     check(pn[live], wp[live], "live p")
     check(bn[:, live], wb[:, live], "live bias")
+
+
+@pytest.mark.parametrize("a,ci", WIDTHS + ((64, 128),))
+@pytest.mark.parametrize("m", (421, 424, 4096))
+def test_ln_gdp_keep_rule_per_tile(hip, a, ci, m):
+    """ln_gdp's mask is its keep, decided per 64-row tile (cuda/volta_gdp.h:114-136): a tile with
+    a row above zero is computed, one with all rows at most zero and one at zero is padded with
+    zeros, and any other tile (all below zero, or NaN) is not written. Rows counts divisible by 8
+    take the 16-byte store path; 424 ends in a 40-row tile whose third 16-row group has 8 rows.
+    The results start as a sentinel, so unwritten columns must still hold it."""
+    rng = rng_for("gdp keep", a, ci, m)
+    x = f16(rng, m, a, s=2.)
+    sc, of = f32(rng, a, s=.1, mean=1.), f32(rng, a, s=.1)
+    wpT, wgT = f16(rng, 2 * ci, a, s=.1), f16(rng, 2 * ci, a, s=.1)
+    bp, bg = f16(rng, 2 * ci, s=.1), f16(rng, 2 * ci, s=.1)
+    mask = (rng.uniform(size=m) > .2).astype(np.float16)
+    mask[rng.uniform(size=m) < .1] = -1
+    tiles = -(-m // 64)
+    kinds = ["compute", "padding", "skip", "padding_mixed", "one_live", "nan", "skip"]
+    for t in range(tiles - 1):
+        rows = slice(64 * t, 64 * t + 64)
+        kind = kinds[t % len(kinds)]
+        if kind == "padding":
+            mask[rows] = 0
+        elif kind == "skip":
+            mask[rows] = -1
+        elif kind == "padding_mixed":
+            mask[rows] = np.where(rng.uniform(size=64) < .5, 0, -1)
+        elif kind == "one_live":
+            mask[rows] = -1
+            mask[64 * t + 17] = 0.5
+        elif kind == "nan":
+            mask[rows] = np.nan
+    tx, tsc, tof, twp, tbp, twg, tbg, tmask = cu(x, sc, of, wpT, bp, wgT, bg, mask)
+    left = torch.full((ci, m), 7.0, dtype=torch.float16, device="cuda")
+    right = torch.full((ci, m), 7.0, dtype=torch.float16, device="cuda")
+    from colabfold_legacy_kernels import hip as h
+    bufs = [h.buffer(t) for t in (tx, tsc, tof, twp, tbp, twg, tbg, tmask, left, right)]
+    h._check(h.lib().clk_ln_gdp(h._stream(tx), *map(h._ref, bufs), EPS))
+    wl, wr = orf.ln_gdp(x, sc, of, wpT, bp, wgT, bg, mask, EPS)
+    for got, want, label in ((npy(left), wl, "left"), (npy(right), wr, "right")):
+        unwritten = np.isnan(want)
+        assert unwritten.any() == ("skip" in kinds[:tiles - 1]), label
+        assert (got[unwritten] == 7.0).all(), label + ": a skipped tile was written"
+        check(got[~unwritten], want[~unwritten], label)
+        padded = np.zeros(want.shape, bool)
+        for t in range(tiles - 1):
+            if kinds[t % len(kinds)] in ("padding", "padding_mixed"):
+                padded[:, 64 * t:64 * t + 64] = True
+        assert (got[padded] == 0).all() and not np.signbit(got[padded]).any(), label + ": padding not +0"
