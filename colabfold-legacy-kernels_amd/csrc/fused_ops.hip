@@ -26,7 +26,7 @@ constexpr int kFThreads = 256;
 constexpr int kFWaves = kFThreads / kWave;
 constexpr int kTileRows = 64;
 constexpr int kProjThreads = 512;  // the projections' workgroup: 8 waves share the weights
-constexpr int kEpiThreads = 256;   // the tri-mul epilogue's workgroup
+constexpr int kEpiThreads = 512;   // the tri-mul epilogue's workgroup
 // ln_gdp: at K = 64 three 4-wave workgroups fit a CU (LDS and registers), at K = 128 one, which
 // then runs 8 waves
 template <int K>
@@ -486,15 +486,29 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
         }
     };
 
-    // the first whole tile runs before the loop, so that the loop is entered, like every later
-    // iteration, with a tile's stores issued after the rows it prefetched
     int tile = blockIdx.x;
-    if (tile < tiles) fetch(tile);
-    if (tile < full) {
-        body(tile, std::true_type{});
-        tile += gridDim.x;
+    if constexpr (K == 128) {
+        // the first whole tile runs before the loop, and the loop is reachable only through it, so
+        // the loop is entered, like every later iteration, with a tile's stores issued after the
+        // rows it prefetched: the wait at the top of a tile covers the rows and not the stores
+        if (tile < full) {
+            fetch(tile);
+            body(tile, std::true_type{});
+            for (tile += gridDim.x; tile < full; tile += gridDim.x) body(tile, std::true_type{});
+        } else if (tile < tiles) {
+            fetch(tile);
+        }
+    } else {
+        // here a path reaches the loop straight from the fetch, so each tile starts by waiting for
+        // the previous tile's stores as well: with two workgroups per CU and the write stream at
+        // its limit, that measured 4% faster than leaving them in flight
+        if (tile < tiles) fetch(tile);
+        if (tile < full) {
+            body(tile, std::true_type{});
+            tile += gridDim.x;
+        }
+        for (; tile < full; tile += gridDim.x) body(tile, std::true_type{});
     }
-    for (; tile < full; tile += gridDim.x) body(tile, std::true_type{});
     if (tile < tiles) body(tile, std::false_type{});
 }
 
@@ -771,26 +785,54 @@ struct EpiArgs {
     float eps;
 };
 
-template <int C, int CA, bool ADD, int TH, bool PREFETCH>
-__global__ __launch_bounds__(TH) void epilogue_kernel(EpiArgs a) {
-    constexpr int KC = C / 32, KA = CA / 32, TW = TH / kWave;
+// LDS of the tri-mul epilogue: both weights, the two operand tiles, LN parameters, reduction rows
+constexpr size_t epi_lds_bytes(int C, int CA, int O) {
+    return (size_t)(O * C + O * CA + kTileRows * C + kTileRows * CA) * 2 +
+           (size_t)(2 * C + 2 * CA + (kEpiThreads / kTileRows) * kTileRows) * 4;
+}
+
+// Waves per SIMD the epilogue is compiled for: 4 (two workgroups per CU, at most 128 VGPRs) where
+// LDS allows two workgroups and the shape fits 128 VGPRs without spilling, else 2
+constexpr int epi_waves(int C, int CA, int O, bool ADD) {
+    const int sum = C + CA + O;
+    return epi_lds_bytes(C, CA, O) <= 80 * 1024 && !(ADD && sum >= 256) && sum < 320 ? 4 : 2;
+}
+
+// Eight waves; wave w owns column pair w / SPLIT and RBW of the four row blocks. The tile body is
+// straight-line code, so that a wait for a load never waits for the stores issued before it
+// (vmcnt counts loads and stores in issue order, and the compiler's count is that of its weakest
+// path):
+// - the next tile's keep values, x_cm columns, x rows and residual are fetched before this tile's
+//   stores and all waited for (keep decision, both LayerNorms, residual to fp32) in the same
+//   iteration, after the stores, so no fetched register crosses the back edge;
+// - the keep decision of each 32-row half comes from a ballot of the 64 rows (one per lane);
+// - every tile runs both LayerNorms and the GEMMs; padding stores zeros, and the stores of skipped
+//   rows and rows past M are buffer stores at an offset past the tile's end, which the hardware
+//   drops, so no branch skips them.
+template <int C, int CA, int O, bool ADD>
+__global__ __launch_bounds__(kEpiThreads, epi_waves(C, CA, O, ADD))
+void epilogue_kernel(EpiArgs a) {
+    constexpr int TH = kEpiThreads, KC = C / 32, KA = CA / 32, TW = TH / kWave;
     constexpr int kSub = 32;  // the reference's keep granularity here (volta_gdp.h:41)
+    constexpr int NPAIRS = O / 32, SPLIT = TW / NPAIRS, RBW = 4 / SPLIT;
+    static_assert(TW % NPAIRS == 0 && 4 % SPLIT == 0, "whole row blocks per wave");
     // column LayerNorm of x_cm: a thread holds one row's values of one of NQ channel groups
     constexpr int NQ = TH / kTileRows, CQ = C / NQ;
     static_assert(CQ % 8 == 0, "channel groups are whole 16-byte fragments");
+    constexpr uint32_t kDrop = 0x80000000u;  // a store offset past every tile's end
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
-    const int nb = a.O / 16, npairs = a.O / 32;
     half_t* Wo = lds;
-    half_t* Wg = Wo + a.O * C;
-    half_t* Yf = Wg + a.O * CA;
+    half_t* Wg = Wo + O * C;
+    half_t* Yf = Wg + O * CA;
     half_t* Af = Yf + kTileRows * C;
     float* lsc = reinterpret_cast<float*>(Af + kTileRows * CA);
     float* lof = lsc + C;
     float* isc = lof + C;
     float* iof = isc + CA;
     float* red = iof + CA;  // [NQ][64]
-    load_weight_frags<C, true>(Wo, a.woT, a.O, nb);
-    load_weight_frags<CA, true>(Wg, a.wgT, a.O, nb);
+    load_weight_frags<C, true>(Wo, a.woT, O, O / 16);
+    load_weight_frags<CA, true>(Wg, a.wgT, O, O / 16);
     for (int i = threadIdx.x; i < C; i += TH) {
         lsc[i] = a.ln_scale[i];
         lof[i] = a.ln_offset[i];
@@ -799,36 +841,61 @@ __global__ __launch_bounds__(TH) void epilogue_kernel(EpiArgs a) {
         isc[i] = a.in_scale[i];
         iof[i] = a.in_offset[i];
     }
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int r16 = lane & 15, g = lane >> 4;
+    const int cp = wave / SPLIT, rb0 = (wave % SPLIT) * RBW;
+    const int col = 32 * cp + 8 * g;
     const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int G = gridDim.x;
     const int r = threadIdx.x % kTileRows, cq = threadIdx.x / kTileRows;
+    const bool has_keep = a.keep != nullptr;
+    // without a keep the descriptor has no bytes, and its loads return zeros without touching memory
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.keep), 0,
+                                                     has_keep ? (uint32_t)a.M * 2u : 0u, 0x00020000);
 
-    // this thread's x_cm values and x chunks of a tile, one tile ahead of their use
-    RowTile<CA, kTileRows, TH> xt;
-    float v[CQ];
-    const auto fetch = [&](int m0) {
-        fetch_rows<CA, kTileRows>(xt, a.x, a.M, m0);
+    float bov[8], bgv[8];
 #pragma unroll
-        for (int i = 0; i < CQ; ++i) v[i] = m0 + r < a.M ? a.x_cm[(int64_t)(cq * CQ + i) * a.M + m0 + r] : 0.f;
-    };
-    if (PREFETCH && blockIdx.x < tiles) fetch(blockIdx.x * kTileRows);
-    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-        const int m0 = tile * kTileRows;
-        const int w0 = tile_work(a.keep, a.M, m0, kSub, -1.f);
-        const int w1 = tile_work(a.keep, a.M, m0 + kSub, kSub, -1.f);
-        if (w0 != kCompute && w1 != kCompute) {
-            if (!ADD) {  // with add_input the output aliases x, which padding keeps
-                for (int i = threadIdx.x; i < kTileRows * a.O / 8; i += TH) {
-                    const int rr = i / (a.O / 8), c = (i % (a.O / 8)) * 8;
-                    const int w = rr < kSub ? w0 : w1;
-                    if (w == kPadding && m0 + rr < a.M) fst8(a.out + (int64_t)(m0 + rr) * a.O + c, fzero8());
-                }
-            }
-            if (PREFETCH && tile + gridDim.x < tiles) fetch((tile + gridDim.x) * kTileRows);
-            continue;
+    for (int j = 0; j < 8; ++j) {
+        bov[j] = (float)a.bo[col + j];
+        bgv[j] = (float)a.bg[col + j];
+    }
+
+    // tile t's keep value of row m0 + lane, x_cm values, x rows and residual (rows past M repeat
+    // row M - 1; their results are dropped)
+    unsigned short kraw;
+    float v[CQ];
+    RowTile<CA, kTileRows, TH> xt;
+    half8 xa[RBW];
+    const auto fetch = [&](int t) {
+        const int m0 = t * kTileRows;
+        kraw = __builtin_amdgcn_raw_buffer_load_b16(rk, (uint32_t)min(m0 + lane, a.M - 1) * 2u, 0, 0);
+        const int mr = min(m0 + r, a.M - 1);
+#pragma unroll
+        for (int i = 0; i < CQ; ++i) v[i] = a.x_cm[(int64_t)(cq * CQ + i) * a.M + mr];
+        constexpr int TPR = RowTile<CA, kTileRows, TH>::kTPR;
+        const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+        const int mx = min(m0 + row, a.M - 1);
+#pragma unroll
+        for (int j = 0; j < RowTile<CA, kTileRows, TH>::kChunks; ++j)
+            xt.v[j] = fld8(a.x + (int64_t)mx * CA + 8 * (part + TPR * j));
+        if constexpr (ADD) {
+#pragma unroll
+            for (int i = 0; i < RBW; ++i)
+                xa[i] = fld8(a.x + (int64_t)min(m0 + 16 * (rb0 + i) + r16, a.M - 1) * CA + col);
         }
-        if (!PREFETCH) fetch(m0);
+    };
+    // per 32-row half: compute, padding or skip (rows past M count as -1, volta_gdp.h:114-136)
+    int w0 = kCompute, w1 = kCompute;
+    float res[RBW][8];
+    const auto prepare = [&](int t) {
+        const int m0 = t * kTileRows;
+        const float k = m0 + lane < a.M ? (has_keep ? (float)__builtin_bit_cast(half_t, kraw) : 1.f) : -1.f;
+        const uint64_t live = __ballot(k > 0.f), zero = __ballot(k == 0.f);
+        const uint32_t live0 = (uint32_t)live, live1 = (uint32_t)(live >> 32);
+        const uint32_t zero0 = (uint32_t)zero, zero1 = (uint32_t)(zero >> 32);
+        w0 = live0 ? (int)kCompute : zero0 ? (int)kPadding : (int)kSkip;
+        w1 = live1 ? (int)kCompute : zero1 ? (int)kPadding : (int)kSkip;
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < CQ; ++i) s += v[i];
@@ -865,71 +932,73 @@ __global__ __launch_bounds__(TH) void epilogue_kernel(EpiArgs a) {
             fst8(Yf + frag(r >> 4, c >> 2, KC, (r & 15) + 16 * (c & 3)), y);
         }
         ln_rows_to_frags<CA, kTileRows, false, true>(Af, xt, isc, iof, a.eps);
+#pragma unroll
+        for (int i = 0; i < RBW; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) res[i][j] = ADD ? (float)xa[i][j] : 0.f;
         __syncthreads();
-        // with add_input the output aliases x: this tile's x was read (and normalised) above
-        if (PREFETCH && tile + gridDim.x < tiles) fetch((tile + gridDim.x) * kTileRows);
-
-        for (int cp = wave; cp < npairs; cp += TW) {
-            float4v ao[2][4], ag[2][4];
+    };
+    const auto gemm_store = [&](int t) {
+        const int m0 = t * kTileRows;
+        float4v ao[2][RBW], ag[2][RBW];
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb)
+        for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    ao[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
-                    ag[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
-                }
-#pragma unroll
-            for (int ks = 0; ks < KC; ++ks) {
-                half8 yop[4];
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) yop[rb] = fld8(Yf + frag(rb, ks, KC, lane));
-#pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
-                    const half8 w = fld8(Wo + frag(2 * cp + hb, ks, KC, lane));
-#pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) ao[hb][rb] = mfma16x16x32(w, yop[rb], ao[hb][rb]);
-                }
+            for (int i = 0; i < RBW; ++i) {
+                ao[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
+                ag[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
-            for (int ks = 0; ks < KA; ++ks) {
-                half8 aop[4];
+        for (int ks = 0; ks < KC; ++ks) {
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) aop[rb] = fld8(Af + frag(rb, ks, KA, lane));
+            for (int hb = 0; hb < 2; ++hb) {
+                const half8 w = fld8(Wo + frag(2 * cp + hb, ks, KC, lane));
 #pragma unroll
-                for (int hb = 0; hb < 2; ++hb) {
-                    const half8 w = fld8(Wg + frag(2 * cp + hb, ks, KA, lane));
-#pragma unroll
-                    for (int rb = 0; rb < 4; ++rb) ag[hb][rb] = mfma16x16x32(w, aop[rb], ag[hb][rb]);
-                }
-            }
-            const int col = 32 * cp + 8 * g;
-            float bov[8], bgv[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                bov[j] = (float)a.bo[col + j];
-                bgv[j] = (float)a.bg[col + j];
-            }
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
-                const int lr = 16 * rb + r16, row = m0 + lr;
-                const int w = lr < kSub ? w0 : w1;
-                if (row >= a.M || w == kSkip || (ADD && w == kPadding)) continue;
-                half_t* dst = a.out + (int64_t)row * a.O + col;
-                if (w == kPadding) {
-                    fst8(dst, fzero8());
-                    continue;
-                }
-                half8 xa = ADD ? fld8(a.x + (int64_t)row * CA + col) : fzero8();
-                half8 o;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float val = (ao[j >> 2][rb][j & 3] + bov[j]) *
-                                      sigmoid_fast(ag[j >> 2][rb][j & 3] + bgv[j]);
-                    o[j] = (half_t)(val + (float)xa[j]);
-                }
-                fst8(dst, o);
+                for (int i = 0; i < RBW; ++i)
+                    ao[hb][i] = mfma16x16x32(w, fld8(Yf + frag(rb0 + i, ks, KC, lane)), ao[hb][i]);
             }
         }
+#pragma unroll
+        for (int ks = 0; ks < KA; ++ks) {
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const half8 w = fld8(Wg + frag(2 * cp + hb, ks, KA, lane));
+#pragma unroll
+                for (int i = 0; i < RBW; ++i)
+                    ag[hb][i] = mfma16x16x32(w, fld8(Af + frag(rb0 + i, ks, KA, lane)), ag[hb][i]);
+            }
+        }
+        // the tile's rows as one buffer: rows past M lie past its end
+        const uint32_t rows = (uint32_t)min(kTileRows, a.M - m0);
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.out + (int64_t)m0 * O, 0, rows * O * 2u, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < RBW; ++i) {
+            const int rb = rb0 + i;
+            const int w = 16 * rb < kSub ? w0 : w1;
+            const bool store = w == kCompute || (!ADD && w == kPadding);
+            half8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float val = (ao[j >> 2][i][j & 3] + bov[j]) * sigmoid_fast(ag[j >> 2][i][j & 3] + bgv[j]);
+                o[j] = (half_t)(w == kPadding ? 0.f : val + res[i][j]);
+            }
+            const uint32_t off = (uint32_t)((16 * rb + r16) * O + col) * 2u;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= tiles) return;
+    fetch(t);
+    prepare(t);
+    for (;;) {
+        const int nt = t + G;
+        // with add_input the output aliases x: the next tile's rows are not this tile's
+        fetch(min(nt, tiles - 1));
+        gemm_store(t);
+        if (nt >= tiles) break;
+        t = nt;
+        prepare(t);
     }
 }
 
@@ -1156,10 +1225,10 @@ static int launch_fused(const char* what, F kernel, dim3 grid, size_t lds, hipSt
 static bool fused_width(int64_t c) { return c == 64 || c == 128; }
 static bool msa_width(int64_t c) { return fused_width(c) || c == 256; }
 
-static unsigned persistent_grid(int64_t tiles, size_t lds) {
+static unsigned persistent_grid(int64_t tiles, size_t lds, int max_per_cu = 4) {
     const int limit = fused_lds_limit();
-    int per_cu = 2;
-    if (limit > 0 && lds > 0) per_cu = std::max(1, std::min(4, (int)(limit / lds)));
+    int per_cu = std::min(2, max_per_cu);
+    if (limit > 0 && lds > 0) per_cu = std::max(1, std::min(max_per_cu, (int)(limit / lds)));
     const int64_t g = std::min<int64_t>(tiles, (int64_t)fused_cu_count() * per_cu);
     return (unsigned)std::max<int64_t>(g, 1);
 }
@@ -1226,25 +1295,29 @@ extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buff
     return launch_status("ln_gdp");
 }
 
-template <int C, int CA, bool ADD>
+template <int C, int CA, int O, bool ADD>
 static int run_epilogue(const EpiArgs& a, hipStream_t s) {
     constexpr int TH = kEpiThreads;
-    const size_t lds = (size_t)(a.O * C + a.O * CA + kTileRows * C + kTileRows * CA) * 2 +
-                       (size_t)(2 * C + 2 * CA + TH) * 4;
+    constexpr size_t lds = epi_lds_bytes(C, CA, O);
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
-    const dim3 grid(persistent_grid(tiles, lds));
-    constexpr bool PF = C == 128;  // measured: the prefetch pays at C = 128 and costs at 64
-    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, ADD, TH, PF>, grid, lds, s, &a, 0)) return st;
+    // as many workgroups per CU as the registers the kernel is compiled for allow
+    const dim3 grid(persistent_grid(tiles, lds, epi_waves(C, CA, O, ADD) / 2));
+    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, O, ADD>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((epilogue_kernel<C, CA, ADD, TH, PF>), grid, dim3(TH), lds, s, a);
+    hipLaunchKernelGGL((epilogue_kernel<C, CA, O, ADD>), grid, dim3(TH), lds, s, a);
     stage_mark(s, 1);
     return launch_status("trimul_epilogue");
 }
 
+template <int C, int CA>
+static int epilogue_dispatch_o(const EpiArgs& a, bool add, hipStream_t s) {
+    if (a.O == 64) return add ? run_epilogue<C, CA, 64, true>(a, s) : run_epilogue<C, CA, 64, false>(a, s);
+    return add ? run_epilogue<C, CA, 128, true>(a, s) : run_epilogue<C, CA, 128, false>(a, s);
+}
+
 template <int C>
 static int epilogue_dispatch(const EpiArgs& a, int64_t CA, bool add, hipStream_t s) {
-    if (CA == 64) return add ? run_epilogue<C, 64, true>(a, s) : run_epilogue<C, 64, false>(a, s);
-    return add ? run_epilogue<C, 128, true>(a, s) : run_epilogue<C, 128, false>(a, s);
+    return CA == 64 ? epilogue_dispatch_o<C, 64>(a, add, s) : epilogue_dispatch_o<C, 128>(a, add, s);
 }
 
 extern "C" int clk_trimul_epilogue(clk_stream stream, const clk_buffer* x_cm, const clk_buffer* x,
