@@ -1007,7 +1007,10 @@ void epilogue_kernel(EpiArgs a) {
 // out^T = W2^T relu(W1 X^T + b1) + b2 over hidden chunks of 64: the first product's accumulator
 // (rows = hidden units in pair order) is exactly the B operand of the second, so the hidden
 // activation never leaves registers. Weight chunks stream through LDS; a 128-row tile (32 rows a
-// wave) amortises each chunk over 64 MFMAs per wave.
+// wave) amortises each chunk over 64 MFMAs per wave. The biases live in LDS, so no global load is
+// waited for between a chunk's prefetch and its use; the last chunk prefetches the first for the
+// next tile, and at C = 64 (where registers allow) the next tile's rows are fetched during this
+// tile's chunks.
 constexpr int kHid = 64;
 constexpr int kTransRows = 128;
 
@@ -1031,20 +1034,28 @@ struct TransTile {
     static constexpr int kSub = C > 128 ? 32 : 64;        // keep granularity (volta_ops.cu:551-553)
 };
 
+// workgroups per CU the transition is compiled for (two at C = 64, whose registers allow it)
+constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
+
 template <int C, bool ADD>
-__global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
+__global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(TransArgs a) {
     using T = TransTile<C>;
     constexpr int KS = T::KS, NCB = C / 16, NSUB = kTransRows / T::kSub;
+    constexpr bool PF = C == 64;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     half_t* Xf = lds;                          // 8 row blocks
     half_t* W1 = Xf + kTransRows * C;          // hidden chunk of w1, then of w2
     half_t* W2 = W1 + T::kW1;
     float* sc = reinterpret_cast<float*>(W2 + T::kW2);
     float* of = sc + C;
+    float* b2s = of + C;
+    float* b1s = b2s + C;  // [H]
     for (int i = threadIdx.x; i < C; i += kFThreads) {
         sc[i] = a.scale[i];
         of[i] = a.offset[i];
+        b2s[i] = a.b2[i];
     }
+    for (int i = threadIdx.x; i < a.H; i += kFThreads) b1s[i] = a.b1[i];
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int tiles = (a.M + kTransRows - 1) / kTransRows;
@@ -1076,6 +1087,8 @@ __global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
     };
 
     RowTile<C, kTransRows> xt;
+    fetch_w(0);
+    if (PF && blockIdx.x < tiles) fetch_rows<C, kTransRows>(xt, a.x, a.M, blockIdx.x * kTransRows);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const int m0 = tile * kTransRows;
         int work[NSUB];
@@ -1093,10 +1106,11 @@ __global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
                         fst8(a.out + (int64_t)(m0 + r) * C + c, fzero8());
                 }
             }
+            if (PF && tile + (int)gridDim.x < tiles)
+                fetch_rows<C, kTransRows>(xt, a.x, a.M, (tile + gridDim.x) * kTransRows);
             continue;
         }
-        fetch_rows<C, kTransRows>(xt, a.x, a.M, m0);
-        fetch_w(0);
+        if (!PF) fetch_rows<C, kTransRows>(xt, a.x, a.M, m0);
         __syncthreads();
         ln_rows_to_frags<C, kTransRows, false, true>(Xf, xt, sc, of, a.eps);
 
@@ -1115,8 +1129,11 @@ __global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(2 * wave + rb, ks, KS, lane));
+                // issued before the weights, so waiting for those (in issue order) covers these
+                if (PF && tile + (int)gridDim.x < tiles)
+                    fetch_rows<C, kTransRows>(xt, a.x, a.M, (tile + gridDim.x) * kTransRows);
             }
-            if (j + 1 < chunks) fetch_w(j + 1);
+            fetch_w(j + 1 < chunks ? j + 1 : 0);  // the first chunk again for the next tile
 
             // hidden^T for 64 units x this wave's 32 rows
             float4v hacc[4][2];
@@ -1139,7 +1156,7 @@ __global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
             for (int kt = 0; kt < 2; ++kt) {
                 float b1v[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) b1v[e] = (float)a.b1[kHid * j + 32 * kt + 8 * g + e];
+                for (int e = 0; e < 8; ++e) b1v[e] = b1s[kHid * j + 32 * kt + 8 * g + e];
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -1175,7 +1192,7 @@ __global__ __launch_bounds__(kFThreads) void transition_kernel(TransArgs a) {
                 half8 o;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    o[e] = (half_t)(acc[2 * cp + (e >> 2)][rb][e & 3] + (float)a.b2[col + e] + (float)xa[e]);
+                    o[e] = (half_t)(acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + (float)xa[e]);
                 fst8(dst, o);
             }
         }
@@ -1472,9 +1489,9 @@ extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, con
 template <int C, bool ADD>
 static int run_transition(const TransArgs& a, hipStream_t s) {
     using T = TransTile<C>;
-    const size_t lds = (size_t)(kTransRows * C + T::kW1 + T::kW2) * 2 + 2 * C * 4;
+    const size_t lds = (size_t)(kTransRows * C + T::kW1 + T::kW2) * 2 + (size_t)(3 * C + a.H) * 4;
     const int64_t tiles = (a.M + kTransRows - 1) / kTransRows;
-    const dim3 grid(persistent_grid(tiles, lds));
+    const dim3 grid(persistent_grid(tiles, lds, trans_per_cu(C)));
     if (int st = launch_fused("transition", transition_kernel<C, ADD>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
     hipLaunchKernelGGL((transition_kernel<C, ADD>), grid, dim3(kFThreads), lds, s, a);
