@@ -512,6 +512,127 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
     if (tile < tiles) body(tile, std::false_type{});
 }
 
+// The output projection (no LayerNorm, no head rows) as straight-line code, like the tri-mul
+// epilogue: eight waves, wave w owning column pair w / SPLIT and RBW of the four row blocks; the
+// next tile's keep values, rows and residual fetched before this tile's stores and consumed in the
+// same iteration after them; the keep decision from a ballot of the tile's 64 rows; dropped
+// buffer stores for skipped tiles, for padding that must keep the residual the output aliases,
+// and for rows past M.
+template <int K, int N, bool RES>
+__global__ __launch_bounds__(kProjThreads, 4) void outproj_kernel(ProjArgs a) {
+    constexpr int TH = kProjThreads, KS = K / 32, TW = TH / kWave;
+    constexpr int NPAIRS = N / 32, SPLIT = TW / NPAIRS, RBW = 4 / SPLIT;
+    static_assert(TW % NPAIRS == 0 && 4 % SPLIT == 0, "whole row blocks per wave");
+    constexpr uint32_t kDrop = 0x80000000u;  // a store offset past every tile's end
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    half_t* Wf = lds;           // N / 16 paired blocks
+    half_t* Xf = Wf + N * K;    // 4 row blocks
+    load_weight_frags<K, true>(Wf, a.wT, N, N / 16);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int cp = wave / SPLIT, rb0 = (wave % SPLIT) * RBW;
+    const int col = 32 * cp + 8 * g;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int G = gridDim.x;
+    const bool has_keep = a.keep != nullptr;
+    // without a keep the descriptor has no bytes, and its loads return zeros without touching memory
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.keep), 0,
+                                                     has_keep ? (uint32_t)a.M * 2u : 0u, 0x00020000);
+    float bv[8];
+    {
+        const half8 b8 = fld8(a.b + col);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bv[j] = (float)b8[j];
+    }
+
+    // tile t's keep value of row m0 + lane, rows and residual (rows past M repeat row M - 1;
+    // their results are dropped)
+    unsigned short kraw;
+    RowTile<K, kTileRows, TH> xt;
+    half8 rs[RBW];
+    const auto fetch = [&](int t) {
+        const int m0 = t * kTileRows;
+        kraw = __builtin_amdgcn_raw_buffer_load_b16(rk, (uint32_t)min(m0 + lane, a.M - 1) * 2u, 0, 0);
+        constexpr int TPR = RowTile<K, kTileRows, TH>::kTPR;
+        const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+        const int mx = min(m0 + row, a.M - 1);
+#pragma unroll
+        for (int j = 0; j < RowTile<K, kTileRows, TH>::kChunks; ++j)
+            xt.v[j] = fld8(a.x + (int64_t)mx * K + 8 * (part + TPR * j));
+        if constexpr (RES) {
+#pragma unroll
+            for (int i = 0; i < RBW; ++i)
+                rs[i] = fld8(a.residual + (int64_t)min(m0 + 16 * (rb0 + i) + r16, a.M - 1) * N + col);
+        }
+    };
+    // the reference's keep rule for the tile (rows past M count as -1, volta_gdp.h:114-136)
+    int work = kCompute;
+    float resf[RBW][8];
+    const auto prepare = [&](int t) {
+        const int m0 = t * kTileRows;
+        const float k = m0 + lane < a.M ? (has_keep ? (float)__builtin_bit_cast(half_t, kraw) : 1.f) : -1.f;
+        const uint64_t live = __ballot(k > 0.f), zero = __ballot(k == 0.f);
+        work = live ? (int)kCompute : zero ? (int)kPadding : (int)kSkip;
+        __syncthreads();  // the previous tile's operand reads are done
+        ln_rows_to_frags<K, kTileRows, false, false>(Xf, xt, nullptr, nullptr, 0.f);
+#pragma unroll
+        for (int i = 0; i < RBW; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) resf[i][j] = RES ? pin_f32((float)rs[i][j]) : 0.f;  // here, not after the next fetch
+        __syncthreads();
+    };
+    const auto gemm_store = [&](int t) {
+        const int m0 = t * kTileRows;
+        float4v acc[2][RBW];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+            for (int i = 0; i < RBW; ++i) acc[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            half8 xop[RBW];
+#pragma unroll
+            for (int i = 0; i < RBW; ++i) xop[i] = fld8(Xf + frag(rb0 + i, ks, KS, lane));
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const half8 w = fld8(Wf + frag(2 * cp + hb, ks, KS, lane));
+#pragma unroll
+                for (int i = 0; i < RBW; ++i) acc[hb][i] = mfma16x16x32(w, xop[i], acc[hb][i]);
+            }
+        }
+        // the tile's rows as one buffer: rows past M lie past its end
+        const uint32_t rows = (uint32_t)min(kTileRows, a.M - m0);
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.out + (int64_t)m0 * N, 0, rows * N * 2u, 0x00020000);
+        // with a residual the output aliases it, which padding keeps
+        const bool store = work == kCompute || (!RES && work == kPadding);
+#pragma unroll
+        for (int i = 0; i < RBW; ++i) {
+            half8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                o[j] = (half_t)(work == kPadding ? 0.f : acc[j >> 2][i][j & 3] + bv[j] + resf[i][j]);
+            const uint32_t off = (uint32_t)((16 * (rb0 + i) + r16) * N + col) * 2u;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= tiles) return;
+    fetch(t);
+    prepare(t);
+    for (;;) {
+        const int nt = t + G;
+        // the output may alias the residual: the next tile's rows are not this tile's
+        fetch(min(nt, tiles - 1));
+        gemm_store(t);
+        if (nt >= tiles) break;
+        t = nt;
+        prepare(t);
+    }
+}
+
 // ---- ln_gated_dual_proj ---------------------------------------------------------------------
 
 struct LnGdpArgs {
@@ -935,7 +1056,7 @@ void epilogue_kernel(EpiArgs a) {
 #pragma unroll
         for (int i = 0; i < RBW; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) res[i][j] = ADD ? (float)xa[i][j] : 0.f;
+            for (int j = 0; j < 8; ++j) res[i][j] = ADD ? pin_f32((float)xa[i][j]) : 0.f;  // here, not after the next fetch
         __syncthreads();
     };
     const auto gemm_store = [&](int t) {
@@ -1411,6 +1532,19 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     return launch_status(what);
 }
 
+template <int K, int N, bool RES>
+static int run_outproj(const ProjArgs& a, hipStream_t s) {
+    constexpr size_t lds = (size_t)(N * K + kTileRows * K) * 2;
+    const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
+    // two workgroups per CU: the registers the kernel is compiled for allow no more
+    const dim3 grid(persistent_grid(tiles, lds, 2));
+    if (int st = launch_fused("output_projection", outproj_kernel<K, N, RES>, grid, lds, s, &a, 0)) return st;
+    stage_mark(s, 0);
+    hipLaunchKernelGGL((outproj_kernel<K, N, RES>), grid, dim3(kProjThreads), lds, s, a);
+    stage_mark(s, 1);
+    return launch_status("output_projection");
+}
+
 extern "C" int clk_ln_projection(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
                                  const clk_buffer* offset, const clk_buffer* wT, const clk_buffer* wbT,
                                  const clk_buffer* keep, const clk_buffer* p, const clk_buffer* bias,
@@ -1483,7 +1617,13 @@ extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, con
     a.M = (int)M;
     a.n = (int)N;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    return K == 64 ? run_proj<64, false>(a, s, "output_projection") : run_proj<128, false>(a, s, "output_projection");
+#define CLK_OUTPROJ(K_, N_)                                                                            \
+    if (K == K_ && N == N_) {                                                                          \
+        return has_residual ? run_outproj<K_, N_, true>(a, s) : run_outproj<K_, N_, false>(a, s);      \
+    }
+    CLK_OUTPROJ(64, 64) CLK_OUTPROJ(64, 128) CLK_OUTPROJ(128, 64) CLK_OUTPROJ(128, 128)
+#undef CLK_OUTPROJ
+    return invalid("output_projection: K and N must be 64 or 128");
 }
 
 template <int C, bool ADD>
