@@ -195,6 +195,130 @@ __global__ __launch_bounds__(256) void gdp_kernel(GdpArgs a) {
     }
 }
 
+// The same op as a persistent, straight-line kernel for K in {64, 128} and N in {64, 128, 256}:
+// eight waves, wave w owning column pair w / SPLIT (32 outputs) and RBW of a 64-row tile's four
+// row blocks. The wave's A operands (W^T rows of its pair, both matrices) are gathered into
+// registers once; per tile only x passes through LDS, as B-operand fragments. The next tile's rows
+// and mask are fetched before this tile's stores and consumed after them in the same iteration,
+// so no wait for a load covers a store (vmcnt counts both in issue order). Results are 16-byte
+// buffer stores through a per-tile descriptor, so rows past M are dropped without a branch.
+// workgroups per CU the fast kernel is compiled for: its registers allow two at K = 64, one at 128
+constexpr int gdp_per_cu(int K) { return K == 64 ? 2 : 1; }
+
+template <int K, int N, bool SWISH>
+__global__ __launch_bounds__(512, 2 * gdp_per_cu(K)) void gdp_fast_kernel(GdpArgs a) {
+    constexpr int TH = 512, KS = K / 32, TW = TH / kWave, KC = K / 8;
+    constexpr int NPAIRS = N / 32, SPLIT = TW / NPAIRS, RBW = 4 / SPLIT;
+    static_assert(TW % NPAIRS == 0 && 4 % SPLIT == 0, "whole row blocks per wave");
+    constexpr int XCPT = kGdpBM * KC / TH;  // 16-byte chunks of the x tile per thread
+    static_assert(XCPT >= 1 && kGdpBM * KC % TH == 0, "whole chunks per thread");
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+    // block rb, step ks, lane (row 16 rb + lane % 16, k-slots 32 ks + 8 (lane / 16) ..)
+    __shared__ __attribute__((aligned(16))) half_t Xf[kGdpBM * K];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int cp = wave / SPLIT, rb0 = (wave % SPLIT) * RBW;
+    const int col = 32 * cp + 8 * g;
+    const int tiles = (a.M + kGdpBM - 1) / kGdpBM;
+    const int G = gridDim.x;
+
+    // A-operand row r16 of block hb: output column 32 cp + 8 (r16 / 4) + 4 hb + r16 % 4, so the
+    // accumulators give lane group g the 8 consecutive columns col .. col + 7
+    half8 wpa[2][KS], wga[2][KS];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+        const int n = 32 * cp + 8 * (r16 >> 2) + 4 * hb + (r16 & 3);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t k = 32 * ks + 8 * g + e;
+                wpa[hb][ks][e] = a.wp[k * N + n];
+                wga[hb][ks][e] = a.wg[k * N + n];
+            }
+    }
+    float bpv[8], bgv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        bpv[j] = (float)a.bp[col + j];
+        bgv[j] = (float)a.bg[col + j];
+    }
+
+    // tile t's x chunks (rows past M repeat row M - 1; their results are dropped) and the mask of
+    // the lane's output row in each of its row blocks
+    half8 xv[XCPT];
+    half_t mraw[RBW];
+    const auto fetch = [&](int t) {
+        const int m0 = t * kGdpBM;
+#pragma unroll
+        for (int j = 0; j < XCPT; ++j) {
+            const int q = threadIdx.x + TH * j, row = q / KC, c = q % KC;
+            xv[j] = *reinterpret_cast<const half8*>(a.x + (int64_t)min(m0 + row, a.M - 1) * K + 8 * c);
+        }
+#pragma unroll
+        for (int i = 0; i < RBW; ++i) mraw[i] = a.mask[min(m0 + 16 * (rb0 + i) + r16, a.M - 1)];
+    };
+    float mv[RBW];
+    const auto prepare = [&]() {
+        __syncthreads();  // the previous tile's operand reads are done
+#pragma unroll
+        for (int j = 0; j < XCPT; ++j) {
+            const int q = threadIdx.x + TH * j, row = q / KC, c = q % KC;
+            const int l = (row & 15) + 16 * (c & 3);
+            *reinterpret_cast<half8*>(&Xf[(((row >> 4) * KS + (c >> 2)) * kWave + l) * 8]) = xv[j];
+        }
+#pragma unroll
+        for (int i = 0; i < RBW; ++i) mv[i] = pin_f32((float)mraw[i]);  // here, not after the next fetch
+        __syncthreads();
+    };
+    const auto gemm_store = [&](int t) {
+        const int m0 = t * kGdpBM;
+        const uint32_t rows = (uint32_t)min(kGdpBM, a.M - m0);
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.out + (int64_t)m0 * N, 0, rows * N * 2u, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < RBW; ++i) {
+            const int rb = rb0 + i;
+            float4v ap[2], ag[2];
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                ap[hb] = float4v{0.f, 0.f, 0.f, 0.f};
+                ag[hb] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const half8 xb = *reinterpret_cast<const half8*>(&Xf[((rb * KS + ks) * kWave + lane) * 8]);
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) {
+                    ap[hb] = mfma16x16x32(wpa[hb][ks], xb, ap[hb]);
+                    ag[hb] = mfma16x16x32(wga[hb][ks], xb, ag[hb]);
+                }
+            }
+            half8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p = ap[j >> 2][j & 3] + bpv[j];
+                o[j] = (half_t)(mv[i] * p * gdp_act<SWISH>(ag[j >> 2][j & 3] + bgv[j]));
+            }
+            const uint32_t off = (uint32_t)((16 * rb + r16) * N + col) * 2u;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, off, 0, 0);
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= tiles) return;
+    fetch(t);
+    prepare();
+    for (;;) {
+        const int nt = t + G;
+        fetch(min(nt, tiles - 1));
+        gemm_store(t);
+        if (nt >= tiles) break;
+        t = nt;
+        prepare();
+    }
+}
+
 }  // namespace clk
 
 using namespace clk;
@@ -263,6 +387,27 @@ extern "C" int clk_gated_dual_proj(clk_stream stream, int32_t device, const clk_
               static_cast<half_t*>(out->data), (int)M, (int)K, (int)N,
               K % 8 == 0 && aligned16(x->data), aligned16(wp->data) && aligned16(wg->data)};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if ((K == 64 || K == 128) && (N == 64 || N == 128 || N == 256) && aligned16(x->data)) {
+        // persistent: as many workgroups as the registers it is compiled for let a CU hold
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            int v = 0;
+            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+        }
+        const int64_t tiles = (M + kGdpBM - 1) / kGdpBM;
+        const dim3 pgrid((unsigned)std::min<int64_t>(tiles, (int64_t)gdp_per_cu((int)K) * cus));
+#define CLK_GDP_FAST(K_, N_)                                                                           \
+        if (K == K_ && N == N_) {                                                                      \
+            stage_mark(s, 0);                                                                          \
+            if (activation == 0) hipLaunchKernelGGL((gdp_fast_kernel<K_, N_, false>), pgrid, dim3(512), 0, s, a); \
+            else hipLaunchKernelGGL((gdp_fast_kernel<K_, N_, true>), pgrid, dim3(512), 0, s, a);     \
+            stage_mark(s, 1);                                                                          \
+            return launch_status("gated_dual_proj");                                                   \
+        }
+        CLK_GDP_FAST(64, 64) CLK_GDP_FAST(64, 128) CLK_GDP_FAST(64, 256)
+        CLK_GDP_FAST(128, 64) CLK_GDP_FAST(128, 128) CLK_GDP_FAST(128, 256)
+#undef CLK_GDP_FAST
+    }
     const dim3 grid((unsigned)((M + kGdpBM - 1) / kGdpBM), (unsigned)((N + kGdpBN - 1) / kGdpBN));
     if (grid.y > 65535) return invalid("gdp: N too large");
     stage_mark(s, 0);

@@ -45,7 +45,10 @@ def test_layer_norm_constant_rows(hip):
     assert abs_excess(out, np.broadcast_to(of, (4, 128)), fp16_out=True) <= 1e-3
 
 
-@pytest.mark.parametrize("m,k,n", [(100, 64, 128), (300, 128, 64), (1, 64, 8), (130, 37, 72), (64, 256, 256)])
+# K in {64, 128} with N in {64, 128, 256} take the persistent kernel; 20000 rows give each of its
+# workgroups several tiles and end in a 32-row tile
+@pytest.mark.parametrize("m,k,n", [(100, 64, 128), (300, 128, 64), (1, 64, 8), (130, 37, 72), (64, 256, 256),
+                                   (20000, 128, 256), (4100, 64, 64), (70, 128, 128), (129, 64, 256)])
 @pytest.mark.parametrize("act", [0, 1])
 def test_gated_dual_proj(hip, m, k, n, act):
     rng = np.random.default_rng(m + k + n + act)
