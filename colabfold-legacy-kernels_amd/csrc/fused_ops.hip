@@ -878,6 +878,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
     if (t >= tiles) return;
     fetch(t);
     int work = decide(t);
+    __syncthreads();  // the weights and LayerNorm parameters are in LDS (decide has no barrier)
     ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
     __syncthreads();
     for (;;) {

@@ -314,3 +314,24 @@ def test_ln_gdp_keep_rule_per_tile(hip, a, ci, m):
             if kinds[t % len(kinds)] in ("padding", "padding_mixed"):
                 padded[:, 64 * t:64 * t + 64] = True
         assert (got[padded] == 0).all() and not np.signbit(got[padded]).any(), label + ": padding not +0"
+
+
+@pytest.mark.parametrize("a,ci", WIDTHS + ((64, 128),))
+def test_ln_gdp_layer_norm_parameters_of_each_call(hip, a, ci):
+    """Consecutive calls with different LayerNorm scale and offset: each call's first tiles must
+    use its own parameters, not what an earlier call left in LDS (the parameters are staged in
+    LDS at the start of the kernel and read by every wave)."""
+    m = 67600  # divisible by 8: the 16-byte store path, with more tiles than workgroups
+    rng = rng_for("gdp params", a, ci)
+    x = f16(rng, m, a, s=2.)
+    wpT, wgT = f16(rng, 2 * ci, a, s=.1), f16(rng, 2 * ci, a, s=.1)
+    bp, bg = f16(rng, 2 * ci, s=.1), f16(rng, 2 * ci, s=.1)
+    mask = (rng.uniform(size=m) > .1).astype(np.float16)
+    tx, twp, tbp, twg, tbg, tmask = cu(x, wpT, bp, wgT, bg, mask)
+    for call in range(3):
+        sc, of = f32(rng, a, s=.5, mean=1. + call), f32(rng, a, s=.5, mean=call)
+        tsc, tof = cu(sc, of)
+        left, right = hip.ln_gdp(tx, tsc, tof, twp, tbp, twg, tbg, tmask, eps=EPS)
+        wl, wr = orf.ln_gdp(x, sc, of, wpT, bp, wgT, bg, mask, EPS)
+        check(npy(left), wl, "call %d left" % call)
+        check(npy(right), wr, "call %d right" % call)
