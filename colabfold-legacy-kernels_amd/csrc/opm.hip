@@ -34,65 +34,82 @@ struct OpmUpdateArgs {
 constexpr int kUpBM = 64, kUpBN = 64, kUpBK = 32;
 constexpr int kUpXLd = kUpBK + 8, kUpTLd = kUpBN + 8;
 
-// Four waves; wave w owns columns n0 + 16 w .. +15 for all 64 rows (four 16-row blocks).
+// Four waves: waves 2 p and 2 p + 1 own the column pair n0 + 32 p .. +31, rows 0-31 and 32-63 of
+// the tile. The A rows of column block hb are n0 + 32 p + 8 (r / 4) + 4 hb + r % 4, so the
+// accumulators give a lane 8 consecutive columns of one row (16-byte stores). Work items are
+// column-tile-major, with the row tiles of one column tile consecutive on one XCD (xcd_item):
+// they share the t tile, which HBM then serves once. The next K step's chunks are loaded (from
+// clamped addresses, unconditionally) before this step's products, and the epilogue's residual,
+// norm and bias before the K loop, so no wait covers a store.
 __global__ __launch_bounds__(256) void opm_update_kernel(OpmUpdateArgs a) {
     __shared__ __attribute__((aligned(16))) half_t Xs[kUpBM * kUpXLd];
     __shared__ __attribute__((aligned(16))) half_t Ts[kUpBK * kUpTLd];
     const int N = a.D * a.F;
-    const int n0 = blockIdx.x * kUpBN, m0 = blockIdx.y * kUpBM;
+    const int mtiles = (a.B + kUpBM - 1) / kUpBM;
+    const int item = xcd_item(blockIdx.x, gridDim.x);
+    const int m0 = (item % mtiles) * kUpBM, n0 = (item / mtiles) * kUpBN;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
+    const int p = wave >> 1, rh = wave & 1;
 
-    float4v acc[4];
+    // epilogue operands: lane holds out[b][n .. n+7], b = m0 + 32 rh + 16 i + r16, one d (F >= 16)
+    const int n = n0 + 32 * p + 8 * g;
+    const bool nin = n < N;  // N is a multiple of 16: 8 columns are wholly in or out
+    const int nc = min(n, N - 8), d = nc / a.F, f = nc - d * a.F;
+    float bv[8];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) acc[rb] = float4v{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < a.K; k0 += kUpBK) {  // K is a multiple of 32
-        __syncthreads();
-        {
-            const int xr = tid >> 2, xc = (tid & 3) * 8;
-            const int gm = m0 + xr;
-            const half8 xv = gm < a.B ? *reinterpret_cast<const half8*>(a.lhs + (int64_t)gm * a.K + k0 + xc)
-                                      : half8{};
-            *reinterpret_cast<half8*>(&Xs[xr * kUpXLd + xc]) = xv;
-            const int tr = tid >> 3, tc = (tid & 7) * 8;
-            // N = D F is a multiple of 16: a chunk of 8 columns is wholly in or out
-            const half8 tv = n0 + tc < N ? *reinterpret_cast<const half8*>(a.t + (int64_t)(k0 + tr) * N + n0 + tc)
-                                         : half8{};
-            *reinterpret_cast<half8*>(&Ts[tr * kUpTLd + tc]) = tv;
-        }
-        __syncthreads();
-        const half8 top = lds_operand_tr([&](int r) { return Ts + r * kUpTLd; }, g, r16, 16 * wave, 4);
+    for (int j = 0; j < 8; ++j) bv[j] = a.bias[f + j];
+    float den[2];
+    half8 res[2];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            const half8 xb = *reinterpret_cast<const half8*>(&Xs[(16 * rb + r16) * kUpXLd + 8 * g]);
-            acc[rb] = mfma16x16x32(top, xb, acc[rb]);
+    for (int i = 0; i < 2; ++i) {
+        const int b = min(m0 + 32 * rh + 16 * i + r16, a.B - 1);
+        den[i] = a.eps + a.norm[(int64_t)b * a.D + d];
+        res[i] = half8{};
+        if (a.residual != nullptr)  // may alias out: read before any write
+            res[i] = *reinterpret_cast<const half8*>(a.residual + (int64_t)b * N + nc);
+    }
+
+    float4v acc[2][2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
+    // this thread's chunks of each K step: rows past B and columns past N repeat the last ones
+    // (their results are not stored); K is a multiple of 32
+    const int xr = tid >> 2, xc = (tid & 3) * 8, tr = tid >> 3, tc = (tid & 7) * 8;
+    const half_t* xrow = a.lhs + (int64_t)min(m0 + xr, a.B - 1) * a.K + xc;
+    const half_t* tcol = a.t + (int64_t)tr * N + min(n0 + tc, N - 8);
+    half8 xv = *reinterpret_cast<const half8*>(xrow);
+    half8 tv = *reinterpret_cast<const half8*>(tcol);
+    for (int k0 = 0; k0 < a.K; k0 += kUpBK) {
+        __syncthreads();  // the previous step's operand reads are done
+        *reinterpret_cast<half8*>(&Xs[xr * kUpXLd + xc]) = xv;
+        *reinterpret_cast<half8*>(&Ts[tr * kUpTLd + tc]) = tv;
+        __syncthreads();
+        const int kn = min(k0 + kUpBK, a.K - kUpBK);
+        xv = *reinterpret_cast<const half8*>(xrow + kn);
+        tv = *reinterpret_cast<const half8*>(tcol + (int64_t)kn * N);
+        half8 top[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+            top[hb] = lds_operand_tr([&](int r) { return Ts + r * kUpTLd; }, g, r16, 32 * p + 4 * hb, 8);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const half8 xb = *reinterpret_cast<const half8*>(&Xs[(32 * rh + 16 * i + r16) * kUpXLd + 8 * g]);
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) acc[hb][i] = mfma16x16x32(top[hb], xb, acc[hb][i]);
         }
     }
-    // lane holds out[b][n .. n+3], b = m0 + 16 rb + r16, n = n0 + 16 wave + 4 g (one d: F >= 16)
-    const int n = n0 + 16 * wave + 4 * g;
-    if (n >= N) return;
-    const int d = n / a.F, f = n - d * a.F;
-    float bv[4];
+    if (!nin) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bv[i] = a.bias[f + i];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-        const int b = m0 + 16 * rb + r16;
+    for (int i = 0; i < 2; ++i) {
+        const int b = m0 + 32 * rh + 16 * i + r16;
         if (b >= a.B) continue;
-        const float den = a.eps + a.norm[(int64_t)b * a.D + d];
-        const int64_t o = (int64_t)b * N + n;
-        float v[4];
+        half8 h;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (acc[rb][i] + bv[i]) / den;
-        if (a.residual != nullptr) {  // may alias out: read before the write below
-            const half4 r = *reinterpret_cast<const half4*>(a.residual + o);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] += (float)r[i];
-        }
-        half4 h;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = (half_t)v[i];
-        *reinterpret_cast<half4*>(a.out + o) = h;
+        for (int j = 0; j < 8; ++j) h[j] = (half_t)((acc[j >> 2][i][j & 3] + bv[j]) / den[i] + (float)res[i][j]);
+        *reinterpret_cast<half8*>(a.out + (int64_t)b * N + n) = h;
     }
 }
 
@@ -227,7 +244,9 @@ extern "C" int clk_opm_update(clk_stream stream, const clk_buffer* lhs, const cl
                     static_cast<const float*>(bias->data), static_cast<const float*>(norm->data),
                     static_cast<half_t*>(out->data), (int)B, (int)K, (int)D, (int)F, eps};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)((D * F + kUpBN - 1) / kUpBN), (unsigned)((B + kUpBM - 1) / kUpBM));
+    const int64_t items = ((D * F + kUpBN - 1) / kUpBN) * ((B + kUpBM - 1) / kUpBM);
+    if (items > INT32_MAX) return invalid("opm_update: too large");
+    const dim3 grid((unsigned)items);
     stage_mark(s, 0);
     hipLaunchKernelGGL(opm_update_kernel, grid, dim3(256), 0, s, a);
     stage_mark(s, 1);
