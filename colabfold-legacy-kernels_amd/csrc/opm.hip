@@ -31,8 +31,8 @@ struct OpmUpdateArgs {
     float eps;
 };
 
-constexpr int kUpBM = 64, kUpBN = 64, kUpBK = 32;
-constexpr int kUpXLd = kUpBK + 8, kUpTLd = kUpBN + 8;
+constexpr int kUpBM = 64, kUpBN = 64;
+constexpr int kUpTLd = kUpBN + 8;
 
 // Four waves: waves 2 p and 2 p + 1 own the column pair n0 + 32 p .. +31, rows 0-31 and 32-63 of
 // the tile. The A rows of column block hb are n0 + 32 p + 8 (r / 4) + 4 hb + r % 4, so the
@@ -40,10 +40,13 @@ constexpr int kUpXLd = kUpBK + 8, kUpTLd = kUpBN + 8;
 // column-tile-major, with the row tiles of one column tile consecutive on one XCD (xcd_item):
 // they share the t tile, which HBM then serves once. The next K step's chunks are loaded (from
 // clamped addresses, unconditionally) before this step's products, and the epilogue's residual,
-// norm and bias before the K loop, so no wait covers a store.
+// norm and bias before the K loop, so no wait covers a store. A K step is BK deep (128, 64 or 32,
+// the largest that divides K), so each barrier pair covers BK / 32 products per column block.
+template <int BK>
 __global__ __launch_bounds__(256) void opm_update_kernel(OpmUpdateArgs a) {
+    constexpr int kUpXLd = BK + 8, XCPT = BK / 32, TCPT = BK / 32;  // 16-byte chunks per thread
     __shared__ __attribute__((aligned(16))) half_t Xs[kUpBM * kUpXLd];
-    __shared__ __attribute__((aligned(16))) half_t Ts[kUpBK * kUpTLd];
+    __shared__ __attribute__((aligned(16))) half_t Ts[BK * kUpTLd];
     const int N = a.D * a.F;
     const int mtiles = (a.B + kUpBM - 1) / kUpBM;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -75,30 +78,41 @@ __global__ __launch_bounds__(256) void opm_update_kernel(OpmUpdateArgs a) {
     for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
         for (int i = 0; i < 2; ++i) acc[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
-    // this thread's chunks of each K step: rows past B and columns past N repeat the last ones
-    // (their results are not stored); K is a multiple of 32
+    // this thread's chunks of each K step: x chunk (row xr, columns xc + 32 u), t chunk (row tr +
+    // 32 u, columns tc); rows past B and columns past N repeat the last ones (their results are not
+    // stored); K is a multiple of BK
     const int xr = tid >> 2, xc = (tid & 3) * 8, tr = tid >> 3, tc = (tid & 7) * 8;
     const half_t* xrow = a.lhs + (int64_t)min(m0 + xr, a.B - 1) * a.K + xc;
     const half_t* tcol = a.t + (int64_t)tr * N + min(n0 + tc, N - 8);
-    half8 xv = *reinterpret_cast<const half8*>(xrow);
-    half8 tv = *reinterpret_cast<const half8*>(tcol);
-    for (int k0 = 0; k0 < a.K; k0 += kUpBK) {
+    half8 xv[XCPT], tv[TCPT];
+    const auto fetch = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < XCPT; ++u) xv[u] = *reinterpret_cast<const half8*>(xrow + k0 + 32 * u);
+#pragma unroll
+        for (int u = 0; u < TCPT; ++u) tv[u] = *reinterpret_cast<const half8*>(tcol + (int64_t)(k0 + 32 * u) * N);
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < a.K; k0 += BK) {
         __syncthreads();  // the previous step's operand reads are done
-        *reinterpret_cast<half8*>(&Xs[xr * kUpXLd + xc]) = xv;
-        *reinterpret_cast<half8*>(&Ts[tr * kUpTLd + tc]) = tv;
+#pragma unroll
+        for (int u = 0; u < XCPT; ++u) *reinterpret_cast<half8*>(&Xs[xr * kUpXLd + xc + 32 * u]) = xv[u];
+#pragma unroll
+        for (int u = 0; u < TCPT; ++u) *reinterpret_cast<half8*>(&Ts[(tr + 32 * u) * kUpTLd + tc]) = tv[u];
         __syncthreads();
-        const int kn = min(k0 + kUpBK, a.K - kUpBK);
-        xv = *reinterpret_cast<const half8*>(xrow + kn);
-        tv = *reinterpret_cast<const half8*>(tcol + (int64_t)kn * N);
-        half8 top[2];
+        fetch(min(k0 + BK, a.K - BK));
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
-            top[hb] = lds_operand_tr([&](int r) { return Ts + r * kUpTLd; }, g, r16, 32 * p + 4 * hb, 8);
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            half8 top[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const half8 xb = *reinterpret_cast<const half8*>(&Xs[(32 * rh + 16 * i + r16) * kUpXLd + 8 * g]);
+            for (int hb = 0; hb < 2; ++hb)
+                top[hb] = lds_operand_tr([&](int r) { return Ts + (32 * ks + r) * kUpTLd; }, g, r16, 32 * p + 4 * hb, 8);
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) acc[hb][i] = mfma16x16x32(top[hb], xb, acc[hb][i]);
+            for (int i = 0; i < 2; ++i) {
+                const half8 xb =
+                    *reinterpret_cast<const half8*>(&Xs[(32 * rh + 16 * i + r16) * kUpXLd + 32 * ks + 8 * g]);
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb) acc[hb][i] = mfma16x16x32(top[hb], xb, acc[hb][i]);
+            }
         }
     }
     if (!nin) return;
@@ -248,7 +262,13 @@ extern "C" int clk_opm_update(clk_stream stream, const clk_buffer* lhs, const cl
     if (items > INT32_MAX) return invalid("opm_update: too large");
     const dim3 grid((unsigned)items);
     stage_mark(s, 0);
-    hipLaunchKernelGGL(opm_update_kernel, grid, dim3(256), 0, s, a);
+    if (K % 128 == 0) {
+        hipLaunchKernelGGL(opm_update_kernel<128>, grid, dim3(256), 0, s, a);
+    } else if (K % 64 == 0) {
+        hipLaunchKernelGGL(opm_update_kernel<64>, grid, dim3(256), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(opm_update_kernel<32>, grid, dim3(256), 0, s, a);
+    }
     stage_mark(s, 1);
     return launch_status("opm_update");
 }
