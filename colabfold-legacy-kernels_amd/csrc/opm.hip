@@ -161,23 +161,49 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
         for (int j = 0; j < 4; ++j)
             ra[eb][j] = a.right[((int64_t)(4 * g + j) * a.D + d) * kOpmE + opm_e(eb, r16)];
 
-    // the weight rows of channel c: Ws[f][e] = wT[f][32 c + e]
-    const auto stage_w = [&](int buf, int c) {
-        for (int i = tid; i < F * (kOpmE / 8); i += 256) {
+    // The weight rows of channel c (Ws[f][e] = wT[f][32 c + e]) and the left values of a chunk of
+    // 16 channels (Lt[c][b][a] = left[a][b0 + b][c0 + c]) pass through registers one channel
+    // step (weights) or one chunk (left) before they are stored to LDS, so their loads are in
+    // flight during a step's products instead of being waited for at once.
+    constexpr int WCH = F * (kOpmE / 8);                        // 16-byte weight chunks per channel
+    constexpr int WCPT = (WCH + 255) / 256;                     // per thread
+    constexpr int LCPT = kOpmRows * kOpmB * (kOpmChunk / 8) / 256;  // left chunks per thread
+    static_assert(kOpmRows * kOpmB * (kOpmChunk / 8) % 256 == 0, "whole left chunks per thread");
+    half8 wreg[WCPT], lreg[LCPT];
+    const auto fetch_w = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < WCPT; ++u) {
+            const int i = min(tid + 256 * u, WCH - 1);
             const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
-            *reinterpret_cast<half8*>(&Ws[buf][f * kWLd + e8]) =
-                *reinterpret_cast<const half8*>(a.wT + (int64_t)f * a.C * kOpmE + c * kOpmE + e8);
+            wreg[u] = *reinterpret_cast<const half8*>(a.wT + (int64_t)f * a.C * kOpmE + c * kOpmE + e8);
         }
     };
-    // left[a][b0 + b][c0 .. c0 + 15] to Lt[c][b][a], rows b past B zero
-    const auto stage_left = [&](int c0) {
-        for (int i = tid; i < kOpmRows * kOpmB * (kOpmChunk / 8); i += 256) {
-            const int v = i % (kOpmChunk / 8), b = i / (kOpmChunk / 8) % kOpmB, r = i / (kOpmChunk / 8) / kOpmB;
-            const half8 x = b0 + b < a.B
-                                ? *reinterpret_cast<const half8*>(a.left + ((int64_t)r * a.B + b0 + b) * a.C + c0 + 8 * v)
-                                : half8{};
+    const auto store_w = [&](int buf) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) Lt[((8 * v + j) * kOpmB + b) * kLtLd + r] = x[j];
+        for (int u = 0; u < WCPT; ++u) {
+            const int i = tid + 256 * u;
+            if (i < WCH) {
+                const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
+                *reinterpret_cast<half8*>(&Ws[buf][f * kWLd + e8]) = wreg[u];
+            }
+        }
+    };
+    // rows b past B repeat the last row (their results are not stored)
+    const auto fetch_left = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < LCPT; ++u) {
+            const int i = tid + 256 * u;
+            const int v = i % (kOpmChunk / 8), b = i / (kOpmChunk / 8) % kOpmB, r = i / (kOpmChunk / 8) / kOpmB;
+            lreg[u] = *reinterpret_cast<const half8*>(a.left + ((int64_t)r * a.B + min(b0 + b, a.B - 1)) * a.C + c0 + 8 * v);
+        }
+    };
+    const auto store_left = [&]() {
+#pragma unroll
+        for (int u = 0; u < LCPT; ++u) {
+            const int i = tid + 256 * u;
+            const int v = i % (kOpmChunk / 8), b = i / (kOpmChunk / 8) % kOpmB, r = i / (kOpmChunk / 8) / kOpmB;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Lt[((8 * v + j) * kOpmB + b) * kLtLd + r] = lreg[u][j];
         }
     };
 
@@ -185,15 +211,20 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
 #pragma unroll
     for (int fb = 0; fb < FB; ++fb) acc[fb] = float4v{0.f, 0.f, 0.f, 0.f};
 
-    stage_w(0, 0);
+    fetch_left(0);
+    fetch_w(0);
+    store_w(0);
+    fetch_w(min(1, a.C - 1));
     for (int c = 0; c < a.C; ++c) {
         const int cl = c % kOpmChunk, buf = c & 1;
         if (cl == 0) {
             __syncthreads();  // the previous chunk's Lt reads are done
-            stage_left(c);
+            store_left();
+            fetch_left(min(c + kOpmChunk, a.C - kOpmChunk));
         }
-        __syncthreads();  // Lt of this chunk and Ws[buf] of this channel are staged
-        if (c + 1 < a.C) stage_w(buf ^ 1, c + 1);  // read a channel ago, before the barrier above
+        __syncthreads();  // Lt of this chunk and Ws[buf] of this channel are staged; Ws[buf ^ 1] is free
+        store_w(buf ^ 1);                   // channel c + 1, fetched a step ago
+        fetch_w(min(c + 2, a.C - 1));       // channel c + 2
 
         // G^T[e][b] for this channel: B operand L^T (lane column b, k-slots a = 4 g .. 4 g + 3)
         const half4 lb = *reinterpret_cast<const half4*>(&Lt[(cl * kOpmB + r16) * kLtLd + 4 * g]);
