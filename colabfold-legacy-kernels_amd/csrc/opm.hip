@@ -142,7 +142,9 @@ struct OpmOuterArgs {
 // e = 8 g + 4 eb + i, i.e. the k-slots 8 g .. 8 g + 7 of the second product's B operand
 __device__ __forceinline__ int opm_e(int eb, int r) { return 8 * (r >> 2) + 4 * eb + (r & 3); }
 
-template <int F>
+// DPW columns d per wave (1, or 2 where D % 8 == 0): the channel's staged weights and left values
+// then serve DPW times as many outputs per barrier.
+template <int F, int DPW>
 __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
     constexpr int FB = F / 16;
     constexpr int kWLd = kOpmE + 8;  // Ws row stride (halfs)
@@ -150,16 +152,18 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
     __shared__ __attribute__((aligned(16))) half_t Ws[2][F * kWLd];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
-    const int b0 = blockIdx.x * kOpmB, d = blockIdx.y * kOpmD + wave;
+    const int b0 = blockIdx.x * kOpmB, d0 = blockIdx.y * kOpmD * DPW + wave;  // d = d0 + kOpmD j
 
     // right[:, d] as the A operand of the first product: row r of e block eb is e = opm_e(eb, r),
     // k-slots a = 4 g .. 4 g + 3
-    half4 ra[2];
+    half4 ra[DPW][2];
 #pragma unroll
-    for (int eb = 0; eb < 2; ++eb)
+    for (int dj = 0; dj < DPW; ++dj)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            ra[eb][j] = a.right[((int64_t)(4 * g + j) * a.D + d) * kOpmE + opm_e(eb, r16)];
+        for (int eb = 0; eb < 2; ++eb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ra[dj][eb][j] = a.right[((int64_t)(4 * g + j) * a.D + d0 + kOpmD * dj) * kOpmE + opm_e(eb, r16)];
 
     // The weight rows of channel c (Ws[f][e] = wT[f][32 c + e]) and the left values of a chunk of
     // 16 channels (Lt[c][b][a] = left[a][b0 + b][c0 + c]) pass through registers one channel
@@ -207,9 +211,11 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
         }
     };
 
-    float4v acc[FB];
+    float4v acc[DPW][FB];
 #pragma unroll
-    for (int fb = 0; fb < FB; ++fb) acc[fb] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int dj = 0; dj < DPW; ++dj)
+#pragma unroll
+        for (int fb = 0; fb < FB; ++fb) acc[dj][fb] = float4v{0.f, 0.f, 0.f, 0.f};
 
     fetch_left(0);
     fetch_w(0);
@@ -228,30 +234,35 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
 
         // G^T[e][b] for this channel: B operand L^T (lane column b, k-slots a = 4 g .. 4 g + 3)
         const half4 lb = *reinterpret_cast<const half4*>(&Lt[(cl * kOpmB + r16) * kLtLd + 4 * g]);
-        half8 gop;
+        half8 gop[DPW];
 #pragma unroll
-        for (int eb = 0; eb < 2; ++eb) {
-            const float4v gt = mfma16x16x16(ra[eb], lb, float4v{0.f, 0.f, 0.f, 0.f});
+        for (int dj = 0; dj < DPW; ++dj)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) gop[4 * eb + i] = (half_t)gt[i];  // the f16 outer product
-        }
+            for (int eb = 0; eb < 2; ++eb) {
+                const float4v gt = mfma16x16x16(ra[dj][eb], lb, float4v{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gop[dj][4 * eb + i] = (half_t)gt[i];  // the f16 outer product
+            }
         // out^T[f][b] += W^T G^T: A row r of f block fb is f = 16 fb + r, k-slots e = 8 g + j
 #pragma unroll
         for (int fb = 0; fb < FB; ++fb) {
             const half8 w = *reinterpret_cast<const half8*>(&Ws[buf][(16 * fb + r16) * kWLd + 8 * g]);
-            acc[fb] = mfma16x16x32(w, gop, acc[fb]);
+#pragma unroll
+            for (int dj = 0; dj < DPW; ++dj) acc[dj][fb] = mfma16x16x32(w, gop[dj], acc[dj][fb]);
         }
     }
     // lane holds out[b][d][f .. f+3], b = b0 + r16, f = 16 fb + 4 g
     const int b = b0 + r16;
     if (b >= a.B) return;
 #pragma unroll
-    for (int fb = 0; fb < FB; ++fb) {
-        half4 h;
+    for (int dj = 0; dj < DPW; ++dj)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[i] = (half_t)acc[fb][i];
-        *reinterpret_cast<half4*>(a.out + ((int64_t)b * a.D + d) * F + 16 * fb + 4 * g) = h;
-    }
+        for (int fb = 0; fb < FB; ++fb) {
+            half4 h;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) h[i] = (half_t)acc[dj][fb][i];
+            *reinterpret_cast<half4*>(a.out + ((int64_t)b * a.D + d0 + kOpmD * dj) * F + 16 * fb + 4 * g) = h;
+        }
 }
 
 static bool opm_width(int64_t f) { return f == 16 || f == 32 || f == 64 || f == 128; }
@@ -329,14 +340,19 @@ extern "C" int clk_opm_outer(clk_stream stream, const clk_buffer* left, const cl
                    static_cast<const half_t*>(wT->data), static_cast<half_t*>(out->data), (int)B,
                    (int)C, (int)D};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)((B + kOpmB - 1) / kOpmB), (unsigned)(D / kOpmD));
     stage_mark(s, 0);
+    const bool two = D % (2 * kOpmD) == 0;
+    const dim3 grid((unsigned)((B + kOpmB - 1) / kOpmB), (unsigned)(D / (kOpmD * (two ? 2 : 1))));
+#define CLK_OPM_OUTER(F_)                                                                              \
+    if (two) hipLaunchKernelGGL((opm_outer_kernel<F_, 2>), grid, dim3(256), 0, s, a);                 \
+    else hipLaunchKernelGGL((opm_outer_kernel<F_, 1>), grid, dim3(256), 0, s, a);
     switch (F) {
-    case 16: hipLaunchKernelGGL(opm_outer_kernel<16>, grid, dim3(256), 0, s, a); break;
-    case 32: hipLaunchKernelGGL(opm_outer_kernel<32>, grid, dim3(256), 0, s, a); break;
-    case 64: hipLaunchKernelGGL(opm_outer_kernel<64>, grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(opm_outer_kernel<128>, grid, dim3(256), 0, s, a); break;
+    case 16: CLK_OPM_OUTER(16) break;
+    case 32: CLK_OPM_OUTER(32) break;
+    case 64: CLK_OPM_OUTER(64) break;
+    default: CLK_OPM_OUTER(128) break;
     }
+#undef CLK_OPM_OUTER
     stage_mark(s, 1);
     return launch_status("opm_outer");
 }
