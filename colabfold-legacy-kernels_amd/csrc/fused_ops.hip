@@ -633,6 +633,131 @@ __global__ __launch_bounds__(kProjThreads, 4) void outproj_kernel(ProjArgs a) {
     }
 }
 
+// ln_projection without a keep mask for n in {256, 512}: every store writes whole output rows.
+// Each wave keeps the A operands of its PAIRS column pairs (W^T rows, in pair order) in registers,
+// which leaves LDS free for the 64 x n output tile. A tile's products go to that tile in LDS
+// (16-byte chunk c of row r at chunk c ^ (r % 16), so a wave's writes cover all banks), and after a
+// barrier each wave stores whole rows: one 16-byte chunk per lane, so a store instruction writes
+// one or two contiguous rows (1 KB). The loop is rotated like the other straight-line kernels:
+// the next tile's rows are fetched before this tile's products and stores and normalised after
+// them. The head-bias block (channel-major) is computed and stored by the last wave as before.
+template <int K, int N>
+__global__ __launch_bounds__(kProjThreads, K == 64 ? 4 : 2) void proj_rows_kernel(ProjArgs a) {
+    constexpr int TH = kProjThreads, KS = K / 32, TW = TH / kWave, PAIRS = N / 32 / TW;
+    constexpr int RCH = N / 8;                   // 16-byte chunks of an output row
+    constexpr int RPI = kWave / RCH;             // rows per store instruction
+    constexpr int SPW = kTileRows / (TW * RPI);  // store instructions per wave and tile
+    static_assert(PAIRS >= 1 && N % (32 * TW) == 0 && kWave % RCH == 0, "whole pairs and rows");
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    half_t* Ot = lds;                    // [64][N], swizzled chunks
+    half_t* Xf = Ot + kTileRows * N;     // 4 row blocks
+    half_t* Hf = Xf + kTileRows * K;     // one block of head rows
+    float* sc = reinterpret_cast<float*>(Hf + 16 * K);
+    float* of = sc + K;
+    const bool do_heads = a.heads > 0;
+    if (do_heads) load_weight_frags<K, false>(Hf, a.wbT, a.heads, 1);
+    for (int i = threadIdx.x; i < K; i += TH) {
+        sc[i] = a.scale[i];
+        of[i] = a.offset[i];
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTileRows - 1) / kTileRows;
+    const int G = gridDim.x;
+    const bool heads_wave = do_heads && wave == TW - 1;
+
+    // A row r of block hb of pair cp = wave + TW pp is output column 32 cp + 8 (r / 4) + 4 hb + r % 4
+    half8 wa[PAIRS][2][KS];
+#pragma unroll
+    for (int pp = 0; pp < PAIRS; ++pp)
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const int col = 32 * (wave + pp * TW) + 8 * (r16 >> 2) + 4 * hb + (r16 & 3);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) wa[pp][hb][ks] = fld8(a.wT + (int64_t)col * K + 32 * ks + 8 * g);
+        }
+
+    // rows of tile t (rows past M repeat row M - 1; their results are dropped)
+    RowTile<K, kTileRows, TH> xt;
+    const auto fetch = [&](int t) {
+        constexpr int TPR = RowTile<K, kTileRows, TH>::kTPR;
+        const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
+        const int m = min(t * kTileRows + row, a.M - 1);
+#pragma unroll
+        for (int j = 0; j < RowTile<K, kTileRows, TH>::kChunks; ++j)
+            xt.v[j] = fld8(a.x + (int64_t)m * K + 8 * (part + TPR * j));
+    };
+    const auto prepare = [&]() {
+        __syncthreads();  // the previous tile's operand reads and output-tile reads are done
+        ln_rows_to_frags<K, kTileRows, false, true>(Xf, xt, sc, of, a.eps);
+        __syncthreads();
+    };
+    const auto compute_store = [&](int t) {
+        const int m0 = t * kTileRows;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            half8 xop[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xop[ks] = fld8(Xf + frag(rb, ks, KS, lane));
+            const int row = 16 * rb + r16;
+#pragma unroll
+            for (int pp = 0; pp < PAIRS; ++pp) {
+                float4v acc[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int hb = 0; hb < 2; ++hb) acc[hb] = mfma16x16x32(wa[pp][hb][ks], xop[ks], acc[hb]);
+                half8 o;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = (half_t)acc[j >> 2][j & 3];
+                const int chunk = 4 * (wave + pp * TW) + g;
+                fst8(Ot + row * N + 8 * (chunk ^ (row & 15)), o);
+            }
+            if (heads_wave) {
+                float4v hacc = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) hacc = mfma16x16x32(fld8(Hf + frag(0, ks, KS, lane)), xop[ks], hacc);
+                const int m = m0 + row;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int h = 4 * g + i;
+                    if (h < a.heads && m < a.M) a.bias[(int64_t)h * a.M + m] = (half_t)hacc[i];
+                }
+            }
+        }
+        __syncthreads();  // the output tile is complete
+        // the tile's rows as one buffer: rows past M lie past its end
+        const uint32_t rows = (uint32_t)min(kTileRows, a.M - m0);
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.out + (int64_t)m0 * N, 0, rows * N * 2u, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < SPW; ++i) {
+            const int row = (i * TW + wave) * RPI + lane / RCH, chunk = lane % RCH;
+            const half8 v = fld8(Ot + row * N + 8 * (chunk ^ (row & 15)));
+            const uint32_t off = (uint32_t)(row * N + 8 * chunk) * 2u;
+            if constexpr (K == 128) {  // nontemporal, as measured for the wide output at c = 128
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, off, 0, 2);
+            } else {
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ro, off, 0, 0);
+            }
+        }
+    };
+
+    int t = blockIdx.x;
+    if (t >= tiles) return;
+    fetch(t);
+    prepare();
+    for (;;) {
+        const int nt = t + G;
+        fetch(min(nt, tiles - 1));
+        compute_store(t);
+        if (nt >= tiles) break;
+        t = nt;
+        prepare();
+    }
+}
+
 // ---- ln_gated_dual_proj ---------------------------------------------------------------------
 
 struct LnGdpArgs {
@@ -1511,6 +1636,23 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     constexpr int TH = kProjThreads, TW = TH / kWave;
     // the fixed-shape kernel: no keep mask, and every column chunk a whole number (1 or 2) of
     // column pairs per wave
+    if constexpr (LN) {
+        // whole-row stores: the weights in registers, the output tile staged in LDS
+        if (a.keep == nullptr && (a.n == 256 || a.n == 512) && a.heads <= 16) {
+            const size_t rlds = (size_t)(kTileRows * a.n + kTileRows * K + 16 * K) * 2 + 2 * K * 4;
+            const dim3 rgrid(persistent_grid(tiles, rlds, K == 64 ? 2 : 1));
+#define CLK_PROJ_ROWS(N_)                                                                              \
+            if (a.n == N_) {                                                                           \
+                if (int st = launch_fused(what, proj_rows_kernel<K, N_>, rgrid, rlds, s, &a, 0)) return st; \
+                stage_mark(s, 0);                                                                      \
+                hipLaunchKernelGGL((proj_rows_kernel<K, N_>), rgrid, dim3(kProjThreads), rlds, s, a);  \
+                stage_mark(s, 1);                                                                      \
+                return launch_status(what);                                                            \
+            }
+            CLK_PROJ_ROWS(256) CLK_PROJ_ROWS(512)
+#undef CLK_PROJ_ROWS
+        }
+    }
     const int pairs = a.cols / 32;
     const bool fast = a.keep == nullptr && a.n % a.cols == 0 && pairs % TW == 0 &&
                       (pairs / TW == 1 || pairs / TW == 2);
