@@ -1281,12 +1281,17 @@ struct TransTile {
     static constexpr int kSub = C > 128 ? 32 : 64;        // keep granularity (volta_ops.cu:551-553)
 };
 
-// workgroups per CU the transition is compiled for (two at C = 64, whose registers allow it)
+// Threads per workgroup: at C = 128 eight waves of one 16-row block each (two waves per SIMD to
+// hide each other's LDS and MFMA latency, where four waves of two row blocks left one), elsewhere
+// four waves of two row blocks. Workgroups per CU the kernel is compiled for: two at C = 64.
+constexpr int trans_threads(int C) { return C == 128 ? 512 : 256; }
 constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
 
-template <int C, bool ADD>
-__global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(TransArgs a) {
+template <int C, bool ADD, int TH>
+__global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_kernel(TransArgs a) {
     using T = TransTile<C>;
+    constexpr int TW = TH / kWave, RB = kTransRows / 16 / TW, kCPT = T::kChunks / TH;
+    static_assert(RB * TW * 16 == kTransRows && kCPT * TH == T::kChunks, "whole row blocks and chunks");
     constexpr int KS = T::KS, NCB = C / 16, NSUB = kTransRows / T::kSub;
     constexpr bool PF = C == 64;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
@@ -1297,12 +1302,12 @@ __global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(
     float* of = sc + C;
     float* b2s = of + C;
     float* b1s = b2s + C;  // [H]
-    for (int i = threadIdx.x; i < C; i += kFThreads) {
+    for (int i = threadIdx.x; i < C; i += TH) {
         sc[i] = a.scale[i];
         of[i] = a.offset[i];
         b2s[i] = a.b2[i];
     }
-    for (int i = threadIdx.x; i < a.H; i += kFThreads) b1s[i] = a.b1[i];
+    for (int i = threadIdx.x; i < a.H; i += TH) b1s[i] = a.b1[i];
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int tiles = (a.M + kTransRows - 1) / kTransRows;
@@ -1310,11 +1315,11 @@ __global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(
 
     // weight chunk j: W1 fragments of hidden rows 64 j + pair_row(hb, r), W2 fragments of output
     // channels pair_row(cb, r) over hidden 64 j + 32 kt + 8 g ..
-    half8 wreg[T::kCPT];
+    half8 wreg[kCPT];
     const auto fetch_w = [&](int j) {
 #pragma unroll
-        for (int u = 0; u < T::kCPT; ++u) {
-            const int i = threadIdx.x + u * kFThreads;
+        for (int u = 0; u < kCPT; ++u) {
+            const int i = threadIdx.x + u * TH;
             const int l = i % kWave, t = i / kWave;
             if (i < T::kW1 / 8) {
                 const int ks = t % KS, hb = t / KS;
@@ -1330,10 +1335,10 @@ __global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(
     };
     const auto store_w = [&]() {
 #pragma unroll
-        for (int u = 0; u < T::kCPT; ++u) fst8(W1 + (threadIdx.x + u * kFThreads) * 8, wreg[u]);
+        for (int u = 0; u < kCPT; ++u) fst8(W1 + (threadIdx.x + u * TH) * 8, wreg[u]);
     };
 
-    RowTile<C, kTransRows> xt;
+    RowTile<C, kTransRows, TH> xt;
     fetch_w(0);
     if (PF && blockIdx.x < tiles) fetch_rows<C, kTransRows>(xt, a.x, a.M, blockIdx.x * kTransRows);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
@@ -1347,7 +1352,7 @@ __global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(
         }
         if (!any) {
             if (!ADD) {
-                for (int i = threadIdx.x; i < kTransRows * C / 8; i += kFThreads) {
+                for (int i = threadIdx.x; i < kTransRows * C / 8; i += TH) {
                     const int r = i / (C / 8), c = (i % (C / 8)) * 8;
                     if (work[r / T::kSub] == kPadding && m0 + r < a.M)
                         fst8(a.out + (int64_t)(m0 + r) * C + c, fzero8());
@@ -1361,51 +1366,51 @@ __global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(
         __syncthreads();
         ln_rows_to_frags<C, kTransRows, false, true>(Xf, xt, sc, of, a.eps);
 
-        float4v acc[NCB][2];
+        float4v acc[NCB][RB];
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) acc[cb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
-        half8 xop[2][KS];
+            for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+        half8 xop[RB][KS];
         for (int j = 0; j < chunks; ++j) {
             __syncthreads();  // the previous chunk's weight reads are done
             store_w();
             __syncthreads();
             if (j == 0) {
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
+                for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                    for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(2 * wave + rb, ks, KS, lane));
+                    for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(RB * wave + rb, ks, KS, lane));
                 // issued before the weights, so waiting for those (in issue order) covers these
                 if (PF && tile + (int)gridDim.x < tiles)
                     fetch_rows<C, kTransRows>(xt, a.x, a.M, (tile + gridDim.x) * kTransRows);
             }
             fetch_w(j + 1 < chunks ? j + 1 : 0);  // the first chunk again for the next tile
 
-            // hidden^T for 64 units x this wave's 32 rows
-            float4v hacc[4][2];
+            // hidden^T for 64 units x this wave's 16 RB rows
+            float4v hacc[4][RB];
 #pragma unroll
             for (int hb = 0; hb < 4; ++hb)
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb) hacc[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                for (int rb = 0; rb < RB; ++rb) hacc[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int hb = 0; hb < 4; ++hb) {
                     const half8 w = fld8(W1 + frag(hb, ks, KS, lane));
 #pragma unroll
-                    for (int rb = 0; rb < 2; ++rb) hacc[hb][rb] = mfma16x16x32(w, xop[rb][ks], hacc[hb][rb]);
+                    for (int rb = 0; rb < RB; ++rb) hacc[hb][rb] = mfma16x16x32(w, xop[rb][ks], hacc[hb][rb]);
                 }
             }
             // relu(. + b1), fp16: slot 8 g + e of step kt is hidden unit 32 kt + 8 g + e
-            half8 hop[2][2];
+            half8 hop[2][RB];
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
                 float b1v[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) b1v[e] = b1s[kHid * j + 32 * kt + 8 * g + e];
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
+                for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         hop[kt][rb][e] = (half_t)fmaxf(hacc[2 * kt + (e >> 2)][rb][e & 3] + b1v[e], 0.f);
@@ -1416,15 +1421,15 @@ __global__ __launch_bounds__(kFThreads, trans_per_cu(C)) void transition_kernel(
                 for (int kt = 0; kt < 2; ++kt) {
                     const half8 w = fld8(W2 + frag(cb, kt, 2, lane));
 #pragma unroll
-                    for (int rb = 0; rb < 2; ++rb) acc[cb][rb] = mfma16x16x32(w, hop[kt][rb], acc[cb][rb]);
+                    for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = mfma16x16x32(w, hop[kt][rb], acc[cb][rb]);
                 }
             }
         }
 
-        // lane: channels 32 (cb/2) + 8 g .. +7 of rows m0 + 32 wave + 16 rb + r16
+        // lane: channels 32 (cb/2) + 8 g .. +7 of rows m0 + 16 (RB wave + rb) + r16
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const int lr = 32 * wave + 16 * rb + r16, row = m0 + lr;
+        for (int rb = 0; rb < RB; ++rb) {
+            const int lr = 16 * (RB * wave + rb) + r16, row = m0 + lr;
             const int w = work[lr / T::kSub];
             if (row >= a.M || w == kSkip || (ADD && w == kPadding)) continue;
 #pragma unroll
@@ -1772,12 +1777,13 @@ extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, con
 template <int C, bool ADD>
 static int run_transition(const TransArgs& a, hipStream_t s) {
     using T = TransTile<C>;
+    constexpr int TH = trans_threads(C);
     const size_t lds = (size_t)(kTransRows * C + T::kW1 + T::kW2) * 2 + (size_t)(3 * C + a.H) * 4;
     const int64_t tiles = (a.M + kTransRows - 1) / kTransRows;
     const dim3 grid(persistent_grid(tiles, lds, trans_per_cu(C)));
-    if (int st = launch_fused("transition", transition_kernel<C, ADD>, grid, lds, s, &a, 0)) return st;
+    if (int st = launch_fused("transition", transition_kernel<C, ADD, TH>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((transition_kernel<C, ADD>), grid, dim3(kFThreads), lds, s, a);
+    hipLaunchKernelGGL((transition_kernel<C, ADD, TH>), grid, dim3(TH), lds, s, a);
     stage_mark(s, 1);
     return launch_status("transition");
 }
