@@ -1256,7 +1256,7 @@ void epilogue_kernel(EpiArgs a) {
 // activation never leaves registers. Weight chunks stream through LDS; a 128-row tile (32 rows a
 // wave) amortises each chunk over 64 MFMAs per wave. The biases live in LDS, so no global load is
 // waited for between a chunk's prefetch and its use; the last chunk prefetches the first for the
-// next tile, and at C = 64 (where registers allow) the next tile's rows are fetched during this
+// next tile, and at C <= 128 (where registers allow) the next tile's rows are fetched during this
 // tile's chunks.
 constexpr int kHid = 64;
 constexpr int kTransRows = 128;
@@ -1293,7 +1293,7 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
     constexpr int TW = TH / kWave, RB = kTransRows / 16 / TW, kCPT = T::kChunks / TH;
     static_assert(RB * TW * 16 == kTransRows && kCPT * TH == T::kChunks, "whole row blocks and chunks");
     constexpr int KS = T::KS, NCB = C / 16, NSUB = kTransRows / T::kSub;
-    constexpr bool PF = C == 64;
+    constexpr bool PF = C <= 128;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     half_t* Xf = lds;                          // 8 row blocks
     half_t* W1 = Xf + kTransRows * C;          // hidden chunk of w1, then of w2
