@@ -1281,10 +1281,11 @@ struct TransTile {
     static constexpr int kSub = C > 128 ? 32 : 64;        // keep granularity (volta_ops.cu:551-553)
 };
 
-// Threads per workgroup: at C = 128 eight waves of one 16-row block each (two waves per SIMD to
-// hide each other's LDS and MFMA latency, where four waves of two row blocks left one), elsewhere
-// four waves of two row blocks. Workgroups per CU the kernel is compiled for: two at C = 64.
-constexpr int trans_threads(int C) { return C == 128 ? 512 : 256; }
+// Threads per workgroup: at C <= 128 eight waves of one 16-row block each (more waves per SIMD to
+// hide each other's LDS and MFMA latency than four waves of two row blocks allow: two instead of
+// one at C = 128, four instead of two at C = 64), at C = 256 four waves of two row blocks.
+// Workgroups per CU the kernel is compiled for: two at C = 64.
+constexpr int trans_threads(int C) { return C <= 128 ? 512 : 256; }
 constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
 
 template <int C, bool ADD, int TH>
