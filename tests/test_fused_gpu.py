@@ -91,7 +91,7 @@ def test_trimul_epilogue(hip, a, ci, m, amp, mean, add):
     check(npy(out), want, "epilogue")
 
 
-@pytest.mark.parametrize("a,n", WIDTHS)
+@pytest.mark.parametrize("a,n", WIDTHS + ((64, 128),))  # (64, 128) with 4 slots: the C4 c = 64 shape
 @pytest.mark.parametrize("m", ROWS)
 @pytest.mark.parametrize("slots,heads", ((4, 4), (3, 8), (0, 8)))
 def test_ln_projection(hip, a, n, m, slots, heads):
