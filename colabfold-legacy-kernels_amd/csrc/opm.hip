@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
     constexpr int FB = F / 16;
     constexpr int kWLd = kOpmE + 8;  // Ws row stride (halfs)
     __shared__ __attribute__((aligned(16))) half_t Lt[kOpmChunk * kOpmB * kLtLd];
-    __shared__ __attribute__((aligned(16))) half_t Ws[2][F * kWLd];
+    __shared__ __attribute__((aligned(16))) half_t Ws[2][2][F * kWLd];  // [buffer][channel of the pair]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int b0 = blockIdx.x * kOpmB, d0 = blockIdx.y * kOpmD * DPW + wave;  // d = d0 + kOpmD j
@@ -165,32 +165,38 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
             for (int j = 0; j < 4; ++j)
                 ra[dj][eb][j] = a.right[((int64_t)(4 * g + j) * a.D + d0 + kOpmD * dj) * kOpmE + opm_e(eb, r16)];
 
-    // The weight rows of channel c (Ws[f][e] = wT[f][32 c + e]) and the left values of a chunk of
-    // 16 channels (Lt[c][b][a] = left[a][b0 + b][c0 + c]) pass through registers one channel
-    // step (weights) or one chunk (left) before they are stored to LDS, so their loads are in
-    // flight during a step's products instead of being waited for at once.
+    // The weight rows of a pair of channels c, c + 1 (Ws[.][h][f][e] = wT[f][32 (c + h) + e]), a
+    // step per barrier, and the left values of a chunk of 16 channels (Lt[c][b][a] =
+    // left[a][b0 + b][c0 + c]) pass through registers one step (weights) or one chunk (left)
+    // before they are stored to LDS, so their loads are in flight during a step's products
+    // instead of being waited for at once.
     constexpr int WCH = F * (kOpmE / 8);                        // 16-byte weight chunks per channel
     constexpr int WCPT = (WCH + 255) / 256;                     // per thread
     constexpr int LCPT = kOpmRows * kOpmB * (kOpmChunk / 8) / 256;  // left chunks per thread
     static_assert(kOpmRows * kOpmB * (kOpmChunk / 8) % 256 == 0, "whole left chunks per thread");
-    half8 wreg[WCPT], lreg[LCPT];
+    half8 wreg[2][WCPT], lreg[LCPT];
+    // channels c and c + 1 (a pair: C is a multiple of 16)
     const auto fetch_w = [&](int c) {
 #pragma unroll
-        for (int u = 0; u < WCPT; ++u) {
-            const int i = min(tid + 256 * u, WCH - 1);
-            const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
-            wreg[u] = *reinterpret_cast<const half8*>(a.wT + (int64_t)f * a.C * kOpmE + c * kOpmE + e8);
-        }
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int u = 0; u < WCPT; ++u) {
+                const int i = min(tid + 256 * u, WCH - 1);
+                const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
+                wreg[h][u] = *reinterpret_cast<const half8*>(a.wT + (int64_t)f * a.C * kOpmE + (c + h) * kOpmE + e8);
+            }
     };
     const auto store_w = [&](int buf) {
 #pragma unroll
-        for (int u = 0; u < WCPT; ++u) {
-            const int i = tid + 256 * u;
-            if (i < WCH) {
-                const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
-                *reinterpret_cast<half8*>(&Ws[buf][f * kWLd + e8]) = wreg[u];
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int u = 0; u < WCPT; ++u) {
+                const int i = tid + 256 * u;
+                if (i < WCH) {
+                    const int f = i / (kOpmE / 8), e8 = (i % (kOpmE / 8)) * 8;
+                    *reinterpret_cast<half8*>(&Ws[buf][h][f * kWLd + e8]) = wreg[h][u];
+                }
             }
-        }
     };
     // rows b past B repeat the last row (their results are not stored)
     const auto fetch_left = [&](int c0) {
@@ -220,35 +226,37 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
     fetch_left(0);
     fetch_w(0);
     store_w(0);
-    fetch_w(min(1, a.C - 1));
-    for (int c = 0; c < a.C; ++c) {
-        const int cl = c % kOpmChunk, buf = c & 1;
+    fetch_w(min(2, a.C - 2));
+    for (int c = 0; c < a.C; c += 2) {
+        const int cl = c % kOpmChunk, buf = (c >> 1) & 1;
         if (cl == 0) {
             __syncthreads();  // the previous chunk's Lt reads are done
             store_left();
             fetch_left(min(c + kOpmChunk, a.C - kOpmChunk));
         }
-        __syncthreads();  // Lt of this chunk and Ws[buf] of this channel are staged; Ws[buf ^ 1] is free
-        store_w(buf ^ 1);                   // channel c + 1, fetched a step ago
-        fetch_w(min(c + 2, a.C - 1));       // channel c + 2
-
-        // G^T[e][b] for this channel: B operand L^T (lane column b, k-slots a = 4 g .. 4 g + 3)
-        const half4 lb = *reinterpret_cast<const half4*>(&Lt[(cl * kOpmB + r16) * kLtLd + 4 * g]);
-        half8 gop[DPW];
+        __syncthreads();  // Lt of this chunk and Ws[buf] of this pair are staged; Ws[buf ^ 1] is free
+        store_w(buf ^ 1);               // channels c + 2, c + 3, fetched a step ago
+        fetch_w(min(c + 4, a.C - 2));   // channels c + 4, c + 5
 #pragma unroll
-        for (int dj = 0; dj < DPW; ++dj)
+        for (int h = 0; h < 2; ++h) {
+            // G^T[e][b] for channel c + h: B operand L^T (lane column b, k-slots a = 4 g .. 4 g + 3)
+            const half4 lb = *reinterpret_cast<const half4*>(&Lt[((cl + h) * kOpmB + r16) * kLtLd + 4 * g]);
+            half8 gop[DPW];
 #pragma unroll
-            for (int eb = 0; eb < 2; ++eb) {
-                const float4v gt = mfma16x16x16(ra[dj][eb], lb, float4v{0.f, 0.f, 0.f, 0.f});
+            for (int dj = 0; dj < DPW; ++dj)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) gop[dj][4 * eb + i] = (half_t)gt[i];  // the f16 outer product
+                for (int eb = 0; eb < 2; ++eb) {
+                    const float4v gt = mfma16x16x16(ra[dj][eb], lb, float4v{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) gop[dj][4 * eb + i] = (half_t)gt[i];  // the f16 outer product
+                }
+            // out^T[f][b] += W^T G^T: A row r of f block fb is f = 16 fb + r, k-slots e = 8 g + j
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) {
+                const half8 w = *reinterpret_cast<const half8*>(&Ws[buf][h][(16 * fb + r16) * kWLd + 8 * g]);
+#pragma unroll
+                for (int dj = 0; dj < DPW; ++dj) acc[dj][fb] = mfma16x16x32(w, gop[dj], acc[dj][fb]);
             }
-        // out^T[f][b] += W^T G^T: A row r of f block fb is f = 16 fb + r, k-slots e = 8 g + j
-#pragma unroll
-        for (int fb = 0; fb < FB; ++fb) {
-            const half8 w = *reinterpret_cast<const half8*>(&Ws[buf][(16 * fb + r16) * kWLd + 8 * g]);
-#pragma unroll
-            for (int dj = 0; dj < DPW; ++dj) acc[dj][fb] = mfma16x16x32(w, gop[dj], acc[dj][fb]);
         }
     }
     // lane holds out[b][d][f .. f+3], b = b0 + r16, f = 16 fb + 4 g
