@@ -6,6 +6,7 @@
   python bench.py --stats-summary DIR            (text summary of a rocprofv3 --stats run)
   python bench.py --traffic-summary FETCH_DIR WRITE_DIR [--calibration-copy MIB]
                                                  (HBM bytes per dispatch from two --pmc runs)
+  python bench.py --counter-summary DIR [DIR ...] (per-kernel means of the counters of --pmc runs)
 
 A step is one attention forward + backward of BASELINE config C3 (MSA row attention with pair
 bias, fp16: N_seq = 512 rows, N_res = 384, H = 8, D = 32): VoltaMma(want_lse) then
@@ -468,6 +469,34 @@ def traffic_summary(fetch_dir, write_dir, mib):
     return "\n".join(lines)
 
 
+def counter_summary(dirs):
+    """Mean per dispatch of every counter in one or more rocprofv3 --pmc runs, for each of the
+    library's kernels (one line per kernel, counters in the order first seen)."""
+    per, names = {}, []
+    for d in dirs:
+        files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+        if not files:
+            raise SystemExit("no counter_collection.csv under " + d)
+        for f in files:
+            for r in csv.DictReader(open(f)):
+                if "clk::" not in r["Kernel_Name"]:
+                    continue
+                c = r["Counter_Name"]
+                if c not in names:
+                    names.append(c)
+                key = (r["Kernel_Name"], c, d, r["Dispatch_Id"])
+                per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    acc = {}
+    for (name, c, _, _), v in per.items():
+        acc.setdefault(name, {}).setdefault(c, []).append(v)
+    lines = []
+    for name in sorted(acc):
+        short = name.replace("void ", "").replace("clk::", "").split("(")[0].replace(" ", "")
+        vals = " ".join("%s=%.4g" % (c, statistics.mean(acc[name][c])) for c in names if c in acc[name])
+        lines.append("%s %s" % (short, vals))
+    return "\n".join(lines)
+
+
 def load_traffic(stage):
     """HBM bytes per dispatch of `stage` from the committed counter summary, or None."""
     try:
@@ -491,12 +520,16 @@ def main():
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB")
     ap.add_argument("--stats-summary", metavar="DIR")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--counter-summary", nargs="+", metavar="DIR")
     args = ap.parse_args()
     if args.stats_summary:
         print(stats_summary(args.stats_summary))
         return
     if args.traffic_summary:
         print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.calibration_copy or 256))
+        return
+    if args.counter_summary:
+        print(counter_summary(args.counter_summary))
         return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU per box; --gpus %d is not supported "
