@@ -165,7 +165,11 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         const int row = c / (DP / 8), col = (c - row * (DP / 8)) * 8;
         kvoff[i] = col < a.D ? (uint32_t)((row * a.ks + col) * 2) : 0x80000000u;
         krow[i] = row;
-        kdst[i] = perm_row(row, 16) * T::kKsLd + col;
+        // K fragment-major: the A operand of key block kb, step ks is 64 consecutive 16-byte chunks
+        // (lane r + 16 g: key 16 (r/4) + 4 kb + r%4, d 32 ks + 8 g ..), so each read is one
+        // conflict-free 1 KB sweep
+        const int kb = (row >> 2) & 3, r16 = 4 * (row >> 4) + (row & 3);
+        kdst[i] = ((kb * T::kKS + (col >> 5)) * kWave + r16 + 16 * ((col >> 3) & 3)) * 8;
         vdst[i] = row * T::kKsLd + col;
     }
     const char* const kb_base = reinterpret_cast<const char*>(a.k + kbase);
@@ -276,12 +280,12 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         float4v s[4][T::kQB];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            // key 16 (r/4) + 4 kb + r%4, stored at row 16 kb + r
+            // key 16 (r/4) + 4 kb + r%4, fragment-major
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < T::kKS; ++ks) {
-                const half8 kop = ld8(&Ks[(16 * kb + r16) * T::kKsLd + 32 * ks + 8 * g]);
+                const half8 kop = ld8(&Ks[((kb * T::kKS + ks) * kWave + lane) * 8]);
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
             }
