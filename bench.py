@@ -2,7 +2,7 @@
 """Benchmark of the ColabFold legacy-kernel hot path on one MI355X (gfx950).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused] [--no-packed]
-                  [--calibration-copy MIB]
+                  [--no-extra] [--calibration-copy MIB]
   python bench.py --stats-summary DIR            (text summary of a rocprofv3 --stats run)
   python bench.py --traffic-summary FETCH_DIR WRITE_DIR [--calibration-copy MIB]
                                                  (HBM bytes per dispatch from two --pmc runs)
@@ -12,7 +12,9 @@ A step is one attention forward + backward of BASELINE config C3 (MSA row attent
 bias, fp16: N_seq = 512 rows, N_res = 384, H = 8, D = 32): VoltaMma(want_lse) then
 VoltaMmaBwd(want_dbias), through the library's C ABI on the current stream, inputs already in
 HBM. value is the step's algorithmic TFLOP/s (14 u flops, u = N H S^2 D: forward 4u, backward
-10u with its recompute of S). Per-kernel durations come from HIP events that the library records
+10u with its recompute of S). The other GPU configs of BASELINE.json are reported beside it as
+objects of the same line: "c2" (triangle attention fwd + bwd, N_res = 256) and "c5" (triangle
+attention forward, N_res = 1024, want_lse off), each with its kernels and roofline. Per-kernel durations come from HIP events that the library records
 on its launch stream at its kernel boundaries (clk_set_stage_events); the roofline object is the
 dominant kernel's, its "traffic" the HBM bytes per dispatch that the committed rocprofv3 counter
 summary (profiles/attention_c3_traffic.txt) measured for that kernel. Reported beside the step:
@@ -111,15 +113,16 @@ def roof_entry(ms_list, flops, byts, **extra):
     return e
 
 
-def attention_algo(ws_bytes):
-    """(flops, bytes) per launch of each C3 kernel. Bytes count every tensor of the kernel's
-    contract read or written once; implementation scratch is listed apart (scratch_bytes)."""
-    u = float(N) * H * S * S * D
-    t = N * H * S * D * 2                   # one fp16 [N,H,S,D] tensor
-    row = N * H * S * 4                     # one fp32 [N,H,S] row statistic
-    bias, km, dbias = H * S * S * 2, N * S, H * S * S * 4
-    sqa, ska = -(-S // 32) * 32, -(-S // 64) * 64
-    biast = H * ska * sqa * 4
+def attention_algo(ws_bytes, n=N, h=H, s=S, d=D):
+    """(flops, bytes, scratch bytes) per launch of each attention kernel at [n, h, s, d]. Bytes
+    count every tensor of the kernel's contract read or written once; implementation scratch is
+    listed apart (scratch_bytes)."""
+    u = float(n) * h * s * s * d
+    t = n * h * s * d * 2                   # one fp16 [N,H,S,D] tensor
+    row = n * h * s * 4                     # one fp32 [N,H,S] row statistic
+    bias, km, dbias = h * s * s * 2, n * s, h * s * s * 4
+    sqa, ska = -(-s // 32) * 32, -(-s // 64) * 64
+    biast = h * ska * sqa * 2
     partial = max(ws_bytes - 2 * row - biast, 0)
     return {
         "attn_fwd": (4 * u, 3 * t + bias + km + t + row, 0),
@@ -131,39 +134,66 @@ def attention_algo(ws_bytes):
     }
 
 
-def bench_attention(torch, hip, steps, warmup, ev):
-    u = float(N) * H * S * S * D
-    scale = D ** -0.5
+def attention_sets(torch, hip, n, h, s, d, mask_frac, bias_std, seed, backward, want_lse):
+    """Two resident buffer sets for one attention config (a step never finds the previous
+    step's tensors in the MALL). mask_frac > 0 pads that share of residues on both axes
+    (kmask = res (x) res, the triangle-attention mask)."""
     g = torch.Generator(device="cuda")
-    g.manual_seed(0)
+    g.manual_seed(seed)
     sets = []
-    for _ in range(2):   # two sets: a step never finds the previous step's tensors in the MALL
-        q, k, v, dout = (torch.randn((N, H, S, D), generator=g, device="cuda").half() for _ in range(4))
-        bias = torch.randn((H, S, S), generator=g, device="cuda").half()
-        kmask = torch.ones((N, S), dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        q, k, v, dout = (torch.randn((n, h, s, d), generator=g, device="cuda").half() for _ in range(4))
+        bias = (torch.randn((h, s, s), generator=g, device="cuda") * bias_std).half()
+        if mask_frac > 0:
+            dead = torch.randperm(s, generator=torch.Generator().manual_seed(seed))[:round(mask_frac * s)]
+            res = torch.ones(s, dtype=torch.uint8)
+            res[dead] = 0
+            kmask = (res[:, None] * res[None, :]).contiguous().cuda() if n == s else \
+                res[None, :].expand(n, s).contiguous().cuda()
+        else:
+            kmask = torch.ones((n, s), dtype=torch.uint8, device="cuda")
         out = torch.empty_like(q)
-        lse = torch.empty((N, H, S), dtype=torch.float32, device="cuda")
-        ws = torch.empty(hip.attention_bwd_workspace(q, k), dtype=torch.uint8, device="cuda")
-        grads = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
-                 torch.empty((H, S, S), dtype=torch.float32, device="cuda"))
+        lse = (torch.empty((n, h, s), dtype=torch.float32, device="cuda") if want_lse
+               else torch.zeros(1, dtype=torch.float32, device="cuda"))
+        ws = grads = None
+        if backward:
+            ws = torch.empty(hip.attention_bwd_workspace(q, k), dtype=torch.uint8, device="cuda")
+            grads = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+                     torch.empty((h, s, s), dtype=torch.float32, device="cuda"))
+        else:
+            del dout
+            dout = None
         sets.append((q, k, v, bias, kmask, dout, out, lse, ws, grads))
+    return sets
+
+
+def bench_attention(torch, hip, steps, warmup, ev, n=N, h=H, s=S, d=D, mask_frac=0.0, bias_std=1.0,
+                    seed=0, backward=True, want_lse=True):
+    """ms per step (VoltaMma, then VoltaMmaBwd(want_dbias) when `backward`), the step's
+    algorithmic flops, and per-kernel timings from the library's stage events."""
+    u = float(n) * h * s * s * d
+    scale = d ** -0.5
+    sets = attention_sets(torch, hip, n, h, s, d, mask_frac, bias_std, seed, backward, want_lse)
 
     def step(st, fwd_ev=None, bwd_ev=None):
         q, k, v, bias, kmask, dout, out, lse, ws, grads = st
         if fwd_ev:
             arm(hip, fwd_ev)
-        hip.attention_fwd(q, k, v, bias, kmask, scale, 64, 32, True, out=out, lse=lse)
-        if bwd_ev:
-            arm(hip, bwd_ev)
-        hip.attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, True, workspace=ws, grads=grads)
-        if bwd_ev:
+        hip.attention_fwd(q, k, v, bias, kmask, scale, 64, 32, want_lse, out=out, lse=lse)
+        if backward:
+            if bwd_ev:
+                arm(hip, bwd_ev)
+            hip.attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, True, workspace=ws,
+                              grads=grads)
+        if fwd_ev or bwd_ev:
             disarm(hip)
 
+    bwd_stages = BWD_STAGES if backward else ()
     for i in range(warmup):
         step(sets[i % 2])
     torch.cuda.synchronize()
     fwd_evs = [ev.create(len(FWD_STAGES) + 1) for _ in range(steps)]
-    bwd_evs = [ev.create(len(BWD_STAGES) + 1) for _ in range(steps)]
+    bwd_evs = [ev.create(len(bwd_stages) + 1) if backward else None for _ in range(steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -172,20 +202,60 @@ def bench_attention(torch, hip, steps, warmup, ev):
     stop.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(stop)
-    per = {name: [] for name in FWD_STAGES + BWD_STAGES}
+    per = {name: [] for name in FWD_STAGES + bwd_stages}
     for fe, be in zip(fwd_evs, bwd_evs):
         for i, name in enumerate(FWD_STAGES):
             per[name].append(ev.elapsed_ms(fe[i], fe[i + 1]))
-        for i, name in enumerate(BWD_STAGES):
+        for i, name in enumerate(bwd_stages):
             per[name].append(ev.elapsed_ms(be[i], be[i + 1]))
-    for e in fwd_evs + bwd_evs:
+    for e in fwd_evs + [b for b in bwd_evs if b]:
         ev.destroy(e)
     disarm(hip)
 
-    algo = attention_algo(sets[0][8].numel())
+    ws_bytes = sets[0][8].numel() if backward else 0
+    algo = attention_algo(ws_bytes, n, h, s, d)
     kernels = {name: roof_entry(per[name], algo[name][0], algo[name][1], scratch_bytes=algo[name][2])
                for name in per}
-    return total_ms / steps, 14 * u, kernels
+    return total_ms / steps, (14 if backward else 4) * u, kernels
+
+
+def roofline_of(kernels):
+    """The roofline object of the dominant (longest) kernel of a step."""
+    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+    kd = kernels[dom]
+    if kd["bound"] == "mfma":
+        roof = {"bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
+    roof["traffic"] = load_traffic(dom)
+    roof["kernel"] = dom
+    roof["ms"] = kd["ms"]
+    return roof
+
+
+# the two other GPU configs of BASELINE.json, reported beside the C3 headline:
+# C2 triangle attention fwd+bwd (N_res = 256, H = 4, bias ~ N(0, 0.5), 5% of residues padded on
+# both axes) and C5 triangle attention forward only (N_res = 1024, H = 4, 8% padded, no lse)
+EXTRA_CONFIGS = {
+    "c2": dict(n=256, h=4, s=256, d=32, mask_frac=0.05, bias_std=0.5, seed=2, backward=True,
+               want_lse=True,
+               workload="C2: triangle attention (starting node), fwd (want_lse) + bwd (want_dbias)"),
+    "c5": dict(n=1024, h=4, s=1024, d=32, mask_frac=0.08, bias_std=1.0, seed=5, backward=False,
+               want_lse=False, workload="C5: triangle attention forward, N_res = 1024, want_lse off"),
+}
+
+
+def bench_extra(torch, hip, ev, name, steps, warmup):
+    cfg = dict(EXTRA_CONFIGS[name])
+    workload = cfg.pop("workload")
+    ms, flops, kernels = bench_attention(torch, hip, steps, warmup, ev, **cfg)
+    t_mfma = flops / (PEAK_TFLOPS * 1e12) * 1e3
+    torch.cuda.empty_cache()
+    return {"workload": workload, "shape": [cfg["n"], cfg["h"], cfg["s"], cfg["d"]],
+            "ms_per_step": round(ms, 5), "tflops": round(flops / ms / 1e9, 2),
+            "frac_mfma_step": round(t_mfma / ms, 4), "flops_per_step": flops,
+            "roofline": roofline_of(kernels), "kernels": kernels}
 
 
 def bench_packed(torch, hip, iters, warmup, ev):
@@ -517,6 +587,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fused", action="store_true")
     ap.add_argument("--no-packed", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C2 and C5 configs")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB")
     ap.add_argument("--stats-summary", metavar="DIR")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
@@ -546,16 +617,7 @@ def main():
     if args.calibration_copy:
         calibration_copy(torch, args.calibration_copy)
     ms_step, flops_step, kernels = bench_attention(torch, hip, args.steps, args.warmup, ev)
-    dom = max(kernels, key=lambda k: kernels[k]["ms"])
-    kd = kernels[dom]
-    if kd["bound"] == "mfma":
-        roof = {"bound": "mfma", "achieved": kd["tflops"], "peak": PEAK_TFLOPS, "unit": "TFLOP/s"}
-    else:
-        roof = {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_GBS, "unit": "GB/s"}
-    roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = load_traffic(dom)
-    roof["kernel"] = dom
-    roof["ms"] = kd["ms"]
+    roof = roofline_of(kernels)
     line = {
         "metric": METRIC,
         "value": round(flops_step / ms_step / 1e9, 2),
@@ -575,6 +637,9 @@ def main():
         "roofline": roof,
         "kernels": kernels,
     }
+    if not args.no_extra:
+        for name in EXTRA_CONFIGS:
+            line[name] = bench_extra(torch, hip, ev, name, args.steps, args.warmup)
     if not args.no_packed:
         line["packed_fwd"] = bench_packed(torch, hip, args.steps, args.warmup, ev)
     if not args.no_fused:

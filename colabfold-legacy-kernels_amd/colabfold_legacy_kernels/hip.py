@@ -85,6 +85,9 @@ def lib():
         handle.clk_version.restype = ctypes.c_char_p
         handle.clk_attention_bwd_workspace_size.argtypes = [ctypes.c_int32, _P, _P]
         handle.clk_attention_bwd_workspace_size.restype = ctypes.c_size_t
+        handle.clk_attention_bwd_plan.argtypes = [ctypes.c_int32] + [ctypes.c_int64] * 5 + \
+            [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32]
+        handle.clk_attention_bwd_plan.restype = ctypes.c_int
         _lib = handle
     return _lib
 
@@ -156,6 +159,13 @@ def attention_packed(p, bias, kmask, gate_bias, scale, block_q=64, block_k=32, c
 def attention_bwd_workspace(q, k):
     return int(lib().clk_attention_bwd_workspace_size(q.device.index, _ref(buffer(q)),
                                                       _ref(buffer(k))))
+
+
+def attention_bwd_plan(n, h, sq, sk, d, device=0):
+    """The backward's launch plan on `device` (a diagnostic for tests and the bench)."""
+    vals = (ctypes.c_int64 * 5)()
+    _check(lib().clk_attention_bwd_plan(device, n, h, sq, sk, d, vals, 5))
+    return dict(zip(("row_groups", "chunk", "chunks", "passes", "windows"), list(vals)))
 
 
 def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, want_dbias=True, workspace=None,

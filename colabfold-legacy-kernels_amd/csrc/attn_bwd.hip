@@ -976,6 +976,18 @@ extern "C" size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buf
     return 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes;
 }
 
+extern "C" int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int64_t Sq,
+                                      int64_t Sk, int64_t D, int64_t* plan, int32_t count) {
+    if (N < 0 || H < 0 || Sq < 0 || Sk < 0 || !bwd_head_dim_ok(D)) {
+        return invalid("attention_bwd_plan: bad shape");
+    }
+    if (plan == nullptr || count < 0) return invalid("attention_bwd_plan: no output array");
+    const BwdPlan p = plan_bwd(device, N, H, Sq, Sk, D);
+    const int64_t vals[] = {p.QG, p.chunk, p.chunks, (p.chunk + p.QG - 1) / p.QG, 1};
+    for (int i = 0; i < count && i < 5; ++i) plan[i] = vals[i];
+    return ok();
+}
+
 extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q,
                                  const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
                                  const clk_buffer* kmask, const clk_buffer* out,

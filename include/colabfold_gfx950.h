@@ -93,6 +93,12 @@ int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q, co
  * backward would reject; the call itself then reports why). */
 size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buffer* q, const clk_buffer* k);
 
+/* Diagnostic, no counterpart in the reference: the backward's launch plan for these shapes on
+ * this device, plan[0..count) = {row groups per dK/dV workgroup, batch rows per workgroup
+ * (chunk), chunks, row passes per workgroup, query windows}. */
+int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int64_t Sq, int64_t Sk,
+                           int64_t D, int64_t* plan, int32_t count);
+
 /* ---- LayerNorm-fused pair-stack projections (reference cuda/volta_fused_ffi.h) --------- */
 
 /* VoltaLnGdp (volta_fused_ffi.h:42-80, handler 337-351): left, right [P/2, M] = the two halves

@@ -16,6 +16,30 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built library")
 
 
+# (test, result, raw max |got - want|, abs excess beyond half an fp16 ulp, rel) of the tests that
+# call record_error; printed as a table at the end of the session
+ERRORS = []
+
+
+def record_error(test, name, got, want, fp16_out=True):
+    """Raw max-abs error, abs_excess and rel of one result, kept for the session summary."""
+    got64, want64 = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    raw = float(np.abs(got64 - want64).max()) if got64.size else 0.0
+    e = abs_excess(got64, want64, fp16_out)
+    r = rel(got64, want64)
+    ERRORS.append((test, name, raw, e, r))
+    return raw, e, r
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not ERRORS:
+        return
+    tr = terminalreporter
+    tr.write_sep("-", "errors against the float64 oracle (raw max abs | beyond half an fp16 ulp | rel)")
+    for test, name, raw, e, r in ERRORS:
+        tr.write_line("%-34s %-6s raw %.3e  excess %.3e  rel %.3e" % (test, name, raw, e, r))
+
+
 def gpu_available():
     try:
         import torch

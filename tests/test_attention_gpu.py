@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import abs_excess, rel
+from conftest import record_error
 from oracle import attention as ora
 
 pytestmark = pytest.mark.gpu
@@ -68,18 +68,20 @@ def run(hip, n=3, h=4, sq=96, sk=96, d=32, seed=0, bq=64, bk=32, kmask=None, qk_
     return got, ref
 
 
-def check(got, ref, label, absolute=True):
+def check(got, ref, label, absolute=True, names=("out", "lse", "dq", "dk", "dv", "dbias")):
+    """rel < REL_TOL for every result and, with `absolute`, the north star's absolute bars on
+    the error beyond each fp16 result's half-ulp rounding; the raw max-abs error of each result
+    is recorded beside them for the session summary."""
     bad = []
-    for name in ("out", "lse", "dq", "dk", "dv", "dbias"):
-        r = rel(got[name], ref[name])
-        msg = "%s %s rel %.2e" % (label, name, r)
+    for name in names:
+        raw, e, r = record_error(label, name, got[name], ref[name],
+                                 fp16_out=name not in ("lse", "dbias"))
         if r >= REL_TOL:
-            bad.append(msg)
+            bad.append("%s %s rel %.2e (raw max abs %.2e)" % (label, name, r, raw))
         if absolute:
             tol = OUT_ATOL if name in ("out", "lse") else GRAD_ATOL
-            e = abs_excess(got[name], ref[name], fp16_out=name not in ("lse", "dbias"))
             if e > tol:
-                bad.append("%s %s abs excess %.2e > %.0e" % (label, name, e, tol))
+                bad.append("%s %s abs excess %.2e > %.0e (raw max abs %.2e)" % (label, name, e, tol, raw))
     assert not bad, "; ".join(bad)
 
 
@@ -124,6 +126,26 @@ def test_tiny_shapes(hip, sq, sk, d):
 def test_batch_sizes(hip, n):
     got, ref = run(hip, n=n, h=2, sq=64, sk=64, d=32)
     check(got, ref, "n=%d" % n)
+
+
+@pytest.mark.parametrize("n,h,s", [(512, 8, 96), (128, 16, 128)])
+def test_multi_pass_dkdv(hip, n, h, s):
+    """Shapes whose dK/dV workgroups take several passes of their row groups: [512, 8, 96]
+    (six passes, a ragged last chunk) and [128, 16, 128] (four row groups, two passes), so the
+    row cursors roll over, the next row's K/V prefetch is used and the dBias partial in LDS
+    accumulates across rows. The results must also repeat bit for bit."""
+    plan = hip.attention_bwd_plan(n, h, s, s, 32)
+    assert plan["passes"] > 1, plan
+    got, ref = run(hip, n=n, h=h, sq=s, sk=s, d=32, seed=3)
+    check(got, ref, "multi-pass n=%d h=%d s=%d" % (n, h, s))
+    q, k, v, bias, km, dout = inputs(n, h, s, s, 32, 3)
+    scale = 32.0 ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale)
+    a = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    b = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    for name, x, y in zip(("dq", "dk", "dv", "dbias"), a, b):
+        assert np.array_equal(x, y), name + " differs between identical calls"
 
 
 def test_repeat_bit_exact(hip):

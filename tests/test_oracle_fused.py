@@ -112,6 +112,75 @@ def test_transition_special_cases():
     np.testing.assert_array_equal(out, np.broadcast_to(inp["b2"], out.shape))
 
 
+def _torch_ln16(x, sc, of):
+    """LayerNorm by torch (float64), rounded to fp16 as the kernels round their GEMM input."""
+    y = torch.nn.functional.layer_norm(torch.from_numpy(np.asarray(x, np.float64)), (x.shape[1],),
+                                       torch.from_numpy(np.asarray(sc, np.float64)),
+                                       torch.from_numpy(np.asarray(of, np.float64)), EPS).numpy()
+    return y.astype(np.float16).astype(np.float64)
+
+
+def test_ln_projection_explicit_sums():
+    """p[m, j] = sum_k fp16(LN x)[m, k] wT[j, k] with no bias term, and the head bias
+    bias[h, m] = sum_k fp16(LN x)[m, k] wbT[h, k] (cuda/volta_ops.cu:503-541,
+    cuda/volta_gdp.h:289-332), from torch's LayerNorm and per-element loops. M, n, heads and K
+    all differ, so a transposed or mis-indexed result cannot pass."""
+    rng = np.random.default_rng(12)
+    m, k, n, heads = 70, 64, 96, 3
+    x = (rng.standard_normal((m, k)) * 2 + 0.3).astype(np.float16)
+    sc = (1 + 0.2 * rng.standard_normal(k)).astype(np.float32)
+    of = (0.2 * rng.standard_normal(k)).astype(np.float32)
+    wT = (0.3 * rng.standard_normal((n, k))).astype(np.float16)
+    wbT = (0.3 * rng.standard_normal((heads, k))).astype(np.float16)
+    p, b = orf.ln_projection(x, sc, of, wT, wbT, None, EPS)
+    assert p.shape == (m, n) and b.shape == (heads, m)
+    y = _torch_ln16(x, sc, of)
+    for mm, j in ((0, 0), (69, 95), (33, 17), (5, 64)):
+        want = sum(y[mm, kk] * float(wT[j, kk]) for kk in range(k))
+        assert abs(p[mm, j] - want) < 1e-10, (mm, j)
+    for h, mm in ((0, 0), (2, 69), (1, 40)):
+        want = sum(y[mm, kk] * float(wbT[h, kk]) for kk in range(k))
+        assert abs(b[h, mm] - want) < 1e-10, (h, mm)
+    # the fp16 rounding of the LN output is observable at this tolerance
+    y_exact = torch.nn.functional.layer_norm(torch.from_numpy(x.astype(np.float64)), (k,),
+                                             torch.from_numpy(sc.astype(np.float64)),
+                                             torch.from_numpy(of.astype(np.float64)), EPS).numpy()
+    unrounded = sum(y_exact[69, kk] * float(wT[95, kk]) for kk in range(k))
+    assert abs(p[69, 95] - unrounded) > 1e-6
+
+
+def test_transition_explicit_loop():
+    """out[m, c] = sum_j fp16(relu(sum_i fp16(LN x)[m, i] w1[i, j] + b1[j])) w2[j, c] + b2[c]
+    (+ x[m, c]) with every weight and bias nonzero (cuda/volta_ops.cu:585-634), the blocked w2T
+    built here by its definition w2T[j][c][i] = w2[64 j + i][c] (volta_fused_ffi.h:216-217)."""
+    rng = np.random.default_rng(13)
+    m, c, hd = 40, 64, 256
+    x = (rng.standard_normal((m, c)) * 2).astype(np.float16)
+    sc = (1 + 0.2 * rng.standard_normal(c)).astype(np.float32)
+    of = (0.2 * rng.standard_normal(c)).astype(np.float32)
+    w1 = (rng.standard_normal((c, hd)) * c ** -0.5).astype(np.float16)
+    b1 = (0.5 * rng.standard_normal(hd)).astype(np.float16)
+    w2 = (rng.standard_normal((hd, c)) * hd ** -0.5).astype(np.float16)
+    b2 = (0.5 * rng.standard_normal(c)).astype(np.float16)
+    w2T = np.zeros((hd // 64, c, 64), np.float16)
+    for j in range(hd // 64):
+        for cc in range(c):
+            for i in range(64):
+                w2T[j, cc, i] = w2[64 * j + i, cc]
+    w1T = np.ascontiguousarray(w1.T)
+    y = _torch_ln16(x, sc, of)
+    for add in (False, True):
+        out = orf.transition(x, sc, of, w1T, b1, w2T, b2, None, EPS, add)
+        for mm, cc in ((0, 0), (39, 63), (17, 30)):
+            hid = [max(sum(y[mm, i] * float(w1[i, j]) for i in range(c)) + float(b1[j]), 0.0)
+                   for j in range(hd)]
+            hid = np.asarray(hid).astype(np.float16).astype(np.float64)
+            want = sum(hid[j] * float(w2[j, cc]) for j in range(hd)) + float(b2[cc])
+            if add:
+                want += float(x[mm, cc])
+            assert abs(out[mm, cc] - want) < 1e-9, (add, mm, cc)
+
+
 def test_trimul_epilogue_elements():
     inp = fused_inputs(7)
     out = orf.trimul_epilogue(inp["x_cm"], inp["x"], inp["sc"], inp["of"], inp["lsc"], inp["lof"], inp["woT"],
