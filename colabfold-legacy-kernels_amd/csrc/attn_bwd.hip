@@ -43,11 +43,16 @@ struct BwdArgs {
     float* qstat;
     half_t* biast;   // workspace [H, SkA, SqA]: bias[h][q][key], 0 outside
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
+    // workspace [2][windows][N][H][Sk][D]: with more than one query window, each window's fp32
+    // dK (unscaled) and dV sums over its queries, added up in window order by dkdv_sum_kernel
+    float* dkv;
     int N, H, Sq, Sk, D;
     int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
     int kblocks;     // ceil(Sk / 64)
     int chunk;       // batch rows per dkdv workgroup
     int chunks;
+    int wtiles;      // 32-query tiles per query window of the dK/dV kernel
+    int windows;     // query windows: ceil(Sq / 32 / wtiles)
     float scale;
     float c1;    // scale log2e, or 1 where |scale log2e| is below 1e-30
     float c1s;   // c1 / log2e: scale, or the stand-in's 1 / log2e
@@ -413,9 +418,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds_raw[];
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
-    // head-major order, as in the forward: an XCD's run of items reads few heads' bias columns
+    // head-major order, as in the forward: an XCD's run of items reads few heads' bias columns;
+    // the key blocks of one query window and chunk are neighbours, so they share Q and dO in L2
     const int kblk = item % a.kblocks, rest = item / a.kblocks;
-    const int c = rest % a.chunks, h = rest / a.chunks;
+    const int win = rest % a.windows, rest2 = rest / a.windows;
+    const int c = rest2 % a.chunks, h = rest2 / a.chunks;
     const int n_begin = c * a.chunk;
     const int n_end = min(a.N, n_begin + a.chunk);
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -426,19 +433,22 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int klocal = kg * 16 + r16;
     const int key = kblk * T::kBK + klocal;
     const bool kin = key < a.Sk;
-    const int qtiles = (a.Sq + T::kBQ - 1) / T::kBQ;  // at least QG (the host plans QG so)
+    // this workgroup's query window: tiles wt0 .. wt0 + qtiles - 1 (at least QG of them, the
+    // host plans QG so); tile indices below are within the window
+    const int wt0 = win * a.wtiles;
+    const int qtiles = min(a.wtiles, (a.Sq + T::kBQ - 1) / T::kBQ - wt0);
     const int qsteps = (qtiles + 1) & ~1;            // steps per row: even, an odd count padded
     const int stagger = qtiles / QG;                 // tile offset between row groups
     const int rows = (n_end - n_begin + QG - 1) / QG;  // row passes of the busiest row group
 
     half_t* const stage0 = reinterpret_cast<half_t*>(lds_raw) + rg * T::kStage;
     constexpr int kBufStride = QG * T::kStage;  // halfs from buffer 0 to buffer 1 of a group
-    // dBias partial [SqA / 4][kBK keys][4 queries]: a 16-lane group's four queries of 16 keys
-    // are one contiguous 256 bytes
+    // dBias partial of the window [32 qtiles / 4][kBK keys][4 queries]: a 16-lane group's four
+    // queries of 16 keys are one contiguous 256 bytes
     float* DBt = reinterpret_cast<float*>(lds_raw + T::kStageBytes);
 
     if constexpr (DBIAS) {
-        for (int i = tid; i < T::kBK * a.SqA; i += T::kThreads) DBt[i] = 0.f;
+        for (int i = tid; i < T::kBK * T::kBQ * qtiles; i += T::kThreads) DBt[i] = 0.f;
     }
 
     const float scale = a.scale;
@@ -500,7 +510,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         cs_o = reinterpret_cast<const char*>(a.dout + nh * a.Sq * a.D);
     };
     const auto fetch_s = [&](Chunks& d) {
-        const int q0 = cs_tile * T::kBQ;
+        const int q0 = (wt0 + cs_tile) * T::kBQ;
         const bool v = cs_rowv && cs_it < qtiles;
         const int bytes = v ? min(T::kBQ, a.Sq - q0) * a.D * 2 : 0;
 #pragma unroll
@@ -524,7 +534,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         bc_st = reinterpret_cast<const char*>(a.qstat + nh * a.SqA * 2);
     };
     const auto fetch_c = [&](half8& d, float& sq) {
-        const int q0 = tile_of(bc_it) * T::kBQ;
+        const int q0 = (wt0 + tile_of(bc_it)) * T::kBQ;
         d = *reinterpret_cast<const half8*>(bt_base + q0 * 2 + bt_off);
         sq = *reinterpret_cast<const float*>(bc_st + q0 * 8 + st_off);
         if (++bc_it == qsteps) {
@@ -583,7 +593,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     // from the chunk set of that parity and refills the set with the step three on (steps past
     // the end load the last step again, unused)
     const auto step = [&](int it, Chunks& next, half8& bt, float& sq) {
-        const int buf = it & 1, q0 = tile_of(it) * T::kBQ;
+        const int buf = it & 1, q0 = tile_of(it) * T::kBQ;  // within the window
         const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
         const half_t* Os = Qs + T::kOs;
@@ -700,28 +710,73 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         if (nv && kin) {
             // the row is done: lane holds d = 32 cc + 8 g .. + 8 of its key for each panel cc
             const int64_t off = ((int64_t)n * a.H + h) * a.Sk * a.D + (int64_t)key * a.D;
+            if (a.windows == 1) {
 #pragma unroll
-            for (int cc = 0; cc < DP / 32; ++cc) {
-                const int d0 = 32 * cc + 8 * g;
-                if (d0 >= a.D) continue;
-                half8 ok, ov;
+                for (int cc = 0; cc < DP / 32; ++cc) {
+                    const int d0 = 32 * cc + 8 * g;
+                    if (d0 >= a.D) continue;
+                    half8 ok, ov;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
-                    ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
+                    for (int j = 0; j < 8; ++j) {
+                        ok[j] = (half_t)(acck[2 * cc + j / 4][j & 3] * scale);
+                        ov[j] = (half_t)accv[2 * cc + j / 4][j & 3];
+                    }
+                    *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
+                    *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
                 }
-                *reinterpret_cast<half8*>(a.dk + off + d0) = ok;
-                *reinterpret_cast<half8*>(a.dv + off + d0) = ov;
+            } else {
+                // this window's sums, fp32, for dkdv_sum_kernel
+                const int64_t plane = (int64_t)a.N * a.H * a.Sk * a.D;
+                float* pk = a.dkv + win * plane + off;
+                float* pv = a.dkv + (a.windows + win) * plane + off;
+#pragma unroll
+                for (int cc = 0; cc < DP / 32; ++cc) {
+                    const int d0 = 32 * cc + 8 * g;
+                    if (d0 >= a.D) continue;
+#pragma unroll
+                    for (int j = 0; j < 8; j += 4) {
+                        *reinterpret_cast<float4*>(pk + d0 + j) =
+                            make_float4(acck[2 * cc + j / 4][0], acck[2 * cc + j / 4][1],
+                                        acck[2 * cc + j / 4][2], acck[2 * cc + j / 4][3]);
+                        *reinterpret_cast<float4*>(pv + d0 + j) =
+                            make_float4(accv[2 * cc + j / 4][0], accv[2 * cc + j / 4][1],
+                                        accv[2 * cc + j / 4][2], accv[2 * cc + j / 4][3]);
+                    }
+                }
             }
         }
     }
 
     if constexpr (DBIAS) {
-        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * T::kBK;
-        for (int i = tid; i < a.SqA * T::kBK; i += T::kThreads) {
+        // the window's rows of the chunk's [SqA][64] partial
+        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * T::kBK +
+                     (int64_t)wt0 * T::kBQ * T::kBK;
+        for (int i = tid; i < qtiles * T::kBQ * T::kBK; i += T::kThreads) {
             const int q = i / T::kBK, kk = i % T::kBK;
-            dst[i] = DBt[(q >> 2) * (4 * T::kBK) + 4 * kk + (q & 3)];  // to [SqA][64]
+            dst[i] = DBt[(q >> 2) * (4 * T::kBK) + 4 * kk + (q & 3)];
         }
+    }
+}
+
+// With more than one query window: dk = fp16(scale * sum of the windows' dK sums), dv = fp16(sum
+// of their dV sums), each summed in window order, four elements per thread (D % 4 == 0).
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_sum_kernel(BwdArgs a) {
+    const int64_t plane = (int64_t)a.N * a.H * a.Sk * a.D;
+    for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < plane;
+         i += (int64_t)gridDim.x * blockDim.x * 4) {
+        float4 sk = *reinterpret_cast<const float4*>(a.dkv + i);
+        float4 sv = *reinterpret_cast<const float4*>(a.dkv + a.windows * plane + i);
+        for (int w = 1; w < a.windows; ++w) {
+            const float4 k = *reinterpret_cast<const float4*>(a.dkv + w * plane + i);
+            const float4 v = *reinterpret_cast<const float4*>(a.dkv + (a.windows + w) * plane + i);
+            sk.x += k.x; sk.y += k.y; sk.z += k.z; sk.w += k.w;
+            sv.x += v.x; sv.y += v.y; sv.z += v.z; sv.w += v.w;
+        }
+        half4 ok = half4{(half_t)(sk.x * a.scale), (half_t)(sk.y * a.scale), (half_t)(sk.z * a.scale),
+                         (half_t)(sk.w * a.scale)};
+        half4 ov = half4{(half_t)sv.x, (half_t)sv.y, (half_t)sv.z, (half_t)sv.w};
+        *reinterpret_cast<half4*>(a.dk + i) = ok;
+        *reinterpret_cast<half4*>(a.dv + i) = ov;
     }
 }
 
@@ -834,9 +889,10 @@ struct BwdPlan {
     int DP = 32;
     int QG = 1;  // query groups of the dK/dV kernel
     int kblocks = 0, chunk = 0, chunks = 0;
+    int wtiles = 1, windows = 1;  // query windows of the dK/dV kernel
     size_t stage_lds = 0, dbias_lds = 0;
     int SqA = 0, SkA = 0;
-    size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0;
+    size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0, dkv_bytes = 0;
     std::string error;
 };
 
@@ -852,40 +908,54 @@ static size_t dkdv_stage_bytes(int DP, int QG) {
 
 // The dK/dV kernel's shape depends only on the problem and the device, never on want_dbias, so
 // dk and dv are bit-identical with and without dbias.
+//
+// Its dBias partial stays in LDS for a whole chunk of rows: 64 keys x the queries of a query
+// window, 8 KB per 32-query tile. Where all of Sq does not fit next to the Q/dO staging, the
+// queries are split into windows of equal tile counts (one more grid dimension); each window's
+// dK and dV sums then go to the workspace in fp32 and dkdv_sum_kernel adds them in window order.
 static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
     BwdPlan p;
     p.DP = D <= 32 ? 32 : D <= 64 ? 64 : 96;
     p.SqA = (int)(((Sq + 31) / 32) * 32);
     p.kblocks = (int)((Sk + 63) / 64);
     p.SkA = p.kblocks * 64;
-    p.dbias_lds = (size_t)64 * p.SqA * sizeof(float);  // the dK/dV kernel's dBias partial
-    const int limit = shared_limit(device);
-    // row groups of the dK/dV kernel: at most the query tiles of a row, which they walk from
-    // staggered starts
+    int limit = shared_limit(device);
+    if (limit <= 0) limit = 64 * 1024;
+    const size_t tile_bytes = (size_t)64 * 32 * sizeof(float);
+    // row groups of the dK/dV kernel: at most the query tiles of a window, which they walk from
+    // staggered starts; the most row groups (waves per CU) first, then the fewest windows
     const int64_t qtiles = std::max<int64_t>((Sq + 31) / 32, 1);
     int qg_max = p.DP == 32 ? 4 : 2;
     while (qg_max > qtiles) qg_max /= 2;
     p.QG = 0;
-    for (int qg = qg_max; qg >= 1; qg /= 2) {
-        const size_t need = dkdv_stage_bytes(p.DP, qg) + p.dbias_lds;
-        if (limit <= 0 || need <= (size_t)limit) {
-            p.QG = qg;
-            break;
-        }
+    for (int qg = qg_max; qg >= 1 && p.QG == 0; qg /= 2) {
+        const size_t stage = dkdv_stage_bytes(p.DP, qg);
+        if (stage + tile_bytes * qg > (size_t)limit) continue;
+        const int64_t wmax = (int64_t)((limit - stage) / tile_bytes);
+        const int64_t windows = (qtiles + wmax - 1) / wmax;
+        const int64_t wtiles = (qtiles + windows - 1) / windows;
+        const int64_t last = qtiles - (windows - 1) * wtiles;
+        if (last < qg) continue;  // every window needs a tile per row group
+        p.QG = qg;
+        p.windows = (int)windows;
+        p.wtiles = (int)wtiles;
     }
     if (p.QG == 0) {
         p.QG = 1;
-        const size_t need = dkdv_stage_bytes(p.DP, 1) + p.dbias_lds;
+        p.windows = (int)qtiles;
+        p.wtiles = 1;
+        const size_t need = dkdv_stage_bytes(p.DP, 1) + tile_bytes;
         p.error = "attention_bwd: dbias needs " + std::to_string(need / 1024) +
                   " KB shared, device allows " + std::to_string(limit / 1024) + " KB";
     }
     p.stage_lds = dkdv_stage_bytes(p.DP, p.QG);
+    p.dbias_lds = tile_bytes * p.wtiles;
     // batch-row chunks: the fewest rounds of workgroups times rows per workgroup
     const size_t per_wg = p.stage_lds + p.dbias_lds;
     const int threads = 256 * p.QG;
-    int per_cu = std::max(1, std::min(2048 / threads, limit > 0 ? (int)(limit / per_wg) : 1));
+    int per_cu = std::max(1, std::min(2048 / threads, (int)(limit / per_wg)));
     const int64_t slots = (int64_t)cu_count(device) * per_cu;
-    const int64_t cols = std::max<int64_t>(H * p.kblocks, 1);
+    const int64_t cols = std::max<int64_t>(H * p.kblocks * p.windows, 1);
     const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
     int64_t best = 1, best_cost = INT64_MAX;
     for (int64_t ch = 1; ch <= Nr; ++ch) {
@@ -907,13 +977,18 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // half of the query terms
     p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(half_t));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
+    p.dkv_bytes = p.windows > 1 ? round256((size_t)2 * p.windows * N * H * Sk * D * sizeof(float)) : 0;
     return p;
+}
+
+static size_t bwd_workspace_bytes(const BwdPlan& p) {
+    return 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes + p.dkv_bytes;
 }
 
 template <int DP, int QG>
 static void launch_dkdv(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bool want_dbias) {
     using T = DkdvTile<DP, QG>;
-    const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks;
+    const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks * p.windows;
     const size_t lds = p.stage_lds + (want_dbias ? p.dbias_lds : 0);
     const void* fn = want_dbias ? reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DP, QG, true>)
                                 : reinterpret_cast<const void*>(&attn_bwd_dkdv_kernel<DP, QG, false>);
@@ -949,6 +1024,11 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     } else {
         launch_dkdv<DP, 1>(stream, a, p, want_dbias);
     }
+    if (p.windows > 1) {
+        const int64_t n4 = (int64_t)a.N * a.H * a.Sk * a.D / 4;
+        const int64_t gs = std::min<int64_t>((n4 + 255) / 256, 8192);
+        hipLaunchKernelGGL(attn_bwd_dkdv_sum_kernel, dim3((unsigned)gs), dim3(256), 0, stream, a);
+    }
     stage_mark(stream, 3);
     if (want_dbias) {
         const int64_t g3 = (int64_t)(a.SqA / 16) * p.kblocks * a.H;
@@ -973,7 +1053,7 @@ extern "C" size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buf
                                                    const clk_buffer* k) {
     if (q == nullptr || k == nullptr || q->rank != 4 || k->rank != 4) return 0;
     const BwdPlan p = plan_bwd(device, q->dims[0], q->dims[1], q->dims[2], k->dims[2], q->dims[3]);
-    return 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes;
+    return bwd_workspace_bytes(p);
 }
 
 extern "C" int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int64_t Sq,
@@ -983,18 +1063,19 @@ extern "C" int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int6
     }
     if (plan == nullptr || count < 0) return invalid("attention_bwd_plan: no output array");
     const BwdPlan p = plan_bwd(device, N, H, Sq, Sk, D);
-    const int64_t vals[] = {p.QG, p.chunk, p.chunks, (p.chunk + p.QG - 1) / p.QG, 1};
+    const int64_t vals[] = {p.QG, p.chunk, p.chunks, (p.chunk + p.QG - 1) / p.QG, p.windows};
     for (int i = 0; i < count && i < 5; ++i) plan[i] = vals[i];
     return ok();
 }
 
-extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q,
-                                 const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
-                                 const clk_buffer* kmask, const clk_buffer* out,
-                                 const clk_buffer* dout, const clk_buffer* lse,
-                                 const clk_buffer* dq, const clk_buffer* dk, const clk_buffer* dv,
-                                 const clk_buffer* dbias, float scale, int32_t want_dbias,
-                                 void* workspace, size_t workspace_bytes) {
+// clk_attention_bwd: validation, plan and launches.
+static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffer* q,
+                              const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
+                              const clk_buffer* kmask, const clk_buffer* out,
+                              const clk_buffer* dout, const clk_buffer* lse, const clk_buffer* dq,
+                              const clk_buffer* dk, const clk_buffer* dv, const clk_buffer* dbias,
+                              float scale, int32_t want_dbias, void* workspace,
+                              size_t workspace_bytes) {
     const clk_buffer* bufs[] = {q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias};
     const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_U8,  CLK_F16,
                          CLK_F16, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F32};
@@ -1025,7 +1106,7 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     const BwdPlan p = plan_bwd(device, N, H, Sq, Sk, D);
     if (want_dbias && !p.error.empty()) return invalid(p.error);
     if (N * H * Sq == 0 && N * H * Sk == 0 && H * Sq * Sk == 0) return ok();  // nothing to write
-    const size_t need = 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes;
+    const size_t need = bwd_workspace_bytes(p);
     if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u)) {
         return fail(CLK_INTERNAL, "volta_mma_bwd: the workspace must be 256-byte aligned and hold " +
                                       std::to_string(need) + " bytes");
@@ -1047,12 +1128,15 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     a.qstat = reinterpret_cast<float*>(ws);
     a.biast = reinterpret_cast<half_t*>(ws + 2 * p.delta_bytes);
     a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
+    a.dkv = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
     a.SqA = p.SqA;
     a.SkA = p.SkA;
     a.kblocks = p.kblocks;
     a.chunk = p.chunk;
     a.chunks = p.chunks;
+    a.wtiles = p.wtiles;
+    a.windows = p.windows;
     a.scale = scale;
     a.c1 = scale * kLog2e;
     a.kscale = fabsf(a.c1) >= 1e-30f;
@@ -1076,4 +1160,15 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
     if (p.DP == 32) return launch_bwd<32>(s, a, p, want_dbias);
     if (p.DP == 64) return launch_bwd<64>(s, a, p, want_dbias);
     return launch_bwd<96>(s, a, p, want_dbias);
+}
+
+extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q,
+                                 const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
+                                 const clk_buffer* kmask, const clk_buffer* out,
+                                 const clk_buffer* dout, const clk_buffer* lse,
+                                 const clk_buffer* dq, const clk_buffer* dk, const clk_buffer* dv,
+                                 const clk_buffer* dbias, float scale, int32_t want_dbias,
+                                 void* workspace, size_t workspace_bytes) {
+    return attention_bwd_impl(stream, device, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
+                              dbias, scale, want_dbias, workspace, workspace_bytes);
 }

@@ -148,6 +148,32 @@ def test_multi_pass_dkdv(hip, n, h, s):
         assert np.array_equal(x, y), name + " differs between identical calls"
 
 
+@pytest.mark.parametrize("n,h,sq,sk,d", [(2, 2, 768, 768, 32), (2, 2, 1024, 1024, 32),
+                                         (3, 2, 520, 200, 32), (2, 2, 544, 544, 64),
+                                         (2, 1, 1000, 700, 96)])
+def test_long_sequences_with_dbias(hip, n, h, sq, sk, d):
+    """Sq past what one LDS-resident dBias partial holds (the reference's backward runs any Sq,
+    cuda/volta_mma_attn_bwd.cu:336-343): the dK/dV kernel splits the queries into windows and
+    sums their dK/dV in window order. Against the oracle, bit-exact on repeat, and dk/dv
+    unchanged without want_dbias."""
+    plan = hip.attention_bwd_plan(n, h, sq, sk, d)
+    assert plan["windows"] > 1, plan
+    got, ref = run(hip, n=n, h=h, sq=sq, sk=sk, d=d, seed=4, bk=64 if d == 64 else 32)
+    check(got, ref, "long n=%d h=%d sq=%d sk=%d d=%d" % (n, h, sq, sk, d))
+    q, k, v, bias, km, dout = inputs(n, h, sq, sk, d, 4)
+    scale = float(d) ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale, 64, 64 if d == 64 else 32)
+    a = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    b = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    off = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale, want_dbias=False))
+    for name, x, y, z in zip(("dq", "dk", "dv", "dbias"), a, b, off):
+        assert np.array_equal(x, y), name + " differs between identical calls"
+        if name != "dbias":
+            assert np.array_equal(x, z), name + " changed when want_dbias was off"
+    assert np.abs(off[3]).max() == 0.0
+
+
 def test_repeat_bit_exact(hip):
     q, k, v, bias, km, dout = inputs(3, 4, 96, 96, 32, 0)
     scale = 32.0 ** -0.5
