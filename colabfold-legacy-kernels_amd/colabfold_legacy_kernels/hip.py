@@ -57,6 +57,8 @@ _SIGNATURES = {
                                  [ctypes.c_float, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32],
     "clk_attention_bwd": [ctypes.c_void_p, ctypes.c_int32] + [_P] * 12 +
                          [ctypes.c_float, ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t],
+    "clk_attention_bwd_noalloc": [ctypes.c_void_p, ctypes.c_int32] + [_P] * 12 +
+                                 [ctypes.c_float, ctypes.c_int32],
     "clk_ln_gdp": [ctypes.c_void_p] + [_P] * 10 + [ctypes.c_float],
     "clk_trimul_epilogue": [ctypes.c_void_p] + [_P] * 12 +
                            [ctypes.c_float, ctypes.c_int32, ctypes.c_int32],
@@ -88,6 +90,8 @@ def lib():
         handle.clk_attention_bwd_plan.argtypes = [ctypes.c_int32] + [ctypes.c_int64] * 5 + \
             [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32]
         handle.clk_attention_bwd_plan.restype = ctypes.c_int
+        handle.clk_attention_bwd_noalloc_scratch_size.argtypes = []
+        handle.clk_attention_bwd_noalloc_scratch_size.restype = ctypes.c_size_t
         _lib = handle
     return _lib
 
@@ -184,6 +188,21 @@ def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, want_dbias=True, 
     _check(lib().clk_attention_bwd(_stream(q), q.device.index, *map(_ref, bufs), float(scale),
                                    int(bool(want_dbias)), ctypes.c_void_p(workspace.data_ptr()),
                                    workspace.numel()))
+    return dq, dk, dv, dbias
+
+
+def attention_bwd_noalloc(q, k, v, bias, kmask, out, dout, lse, scale, want_dbias=True,
+                          grads=None):
+    """VoltaMmaBwd without a workspace: the library's static per-GPU scratch serves instead
+    (clk_attention_bwd_noalloc; calls that overlap on one GPU race for it)."""
+    if grads is None:
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        dbias = torch.empty(bias.shape, dtype=torch.float32, device=q.device)
+    else:
+        dq, dk, dv, dbias = grads
+    bufs = [buffer(t) for t in (q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias)]
+    _check(lib().clk_attention_bwd_noalloc(_stream(q), q.device.index, *map(_ref, bufs),
+                                           float(scale), int(bool(want_dbias))))
     return dq, dk, dv, dbias
 
 

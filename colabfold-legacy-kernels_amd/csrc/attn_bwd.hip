@@ -23,6 +23,8 @@
 //   dbias_kernel  dbias = the chunk partials summed in chunk order.
 #include "clk_common.h"
 
+#include <mutex>
+
 namespace clk {
 
 struct BwdArgs {
@@ -1068,14 +1070,52 @@ extern "C" int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int6
     return ok();
 }
 
-// clk_attention_bwd: validation, plan and launches.
+// The size of the static scratch of clk_attention_bwd_noalloc: enough for BASELINE C3
+// ([512, 8, 384, 32]: 86.3 MiB of query terms, transposed bias and dBias partials).
+constexpr size_t kNoAllocScratchBytes = size_t(96) << 20;
+
+// The scratch of clk_attention_bwd_noalloc, one copy per GPU, held until the process ends. Host
+// code never uses this name as an address: scratch_address() asks the runtime for each device's
+// copy once, with that device current, and every use goes through the pointer it returns.
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+static int scratch_address(int device, void** out) {
+    constexpr int kDevices = 16;
+    static std::mutex mu;
+    static void* ptrs[kDevices] = {};
+    if (device < 0 || device >= kDevices) {
+        return invalid("attention_bwd_noalloc: device " + std::to_string(device) + " out of range");
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[device] == nullptr) {
+        int cur = -1;
+        hipError_t err = hipGetDevice(&cur);
+        if (err == hipSuccess && cur != device) err = hipSetDevice(device);
+        if (err != hipSuccess) {
+            return fail(CLK_INTERNAL, std::string("attention_bwd_noalloc: cannot select device: ") +
+                                          hipGetErrorString(err));
+        }
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != device) (void)hipSetDevice(cur);
+        if (err != hipSuccess || p == nullptr) {
+            return fail(CLK_INTERNAL, std::string("attention_bwd_noalloc: hipGetSymbolAddress: ") +
+                                          hipGetErrorString(err));
+        }
+        ptrs[device] = p;
+    }
+    *out = ptrs[device];
+    return CLK_OK;
+}
+
+// clk_attention_bwd, with its workspace given (noalloc false) or taken from the static scratch.
 static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffer* q,
                               const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
                               const clk_buffer* kmask, const clk_buffer* out,
                               const clk_buffer* dout, const clk_buffer* lse, const clk_buffer* dq,
                               const clk_buffer* dk, const clk_buffer* dv, const clk_buffer* dbias,
                               float scale, int32_t want_dbias, void* workspace,
-                              size_t workspace_bytes) {
+                              size_t workspace_bytes, bool noalloc) {
     const clk_buffer* bufs[] = {q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias};
     const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_U8,  CLK_F16,
                          CLK_F16, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F32};
@@ -1107,6 +1147,15 @@ static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffe
     if (want_dbias && !p.error.empty()) return invalid(p.error);
     if (N * H * Sq == 0 && N * H * Sk == 0 && H * Sq * Sk == 0) return ok();  // nothing to write
     const size_t need = bwd_workspace_bytes(p);
+    if (noalloc) {
+        if (need > kNoAllocScratchBytes) {
+            return invalid("attention_bwd_noalloc: these shapes need " + std::to_string(need) +
+                           " bytes of scratch, the library's static scratch holds " +
+                           std::to_string(kNoAllocScratchBytes));
+        }
+        if (int st = scratch_address(device, &workspace)) return st;
+        workspace_bytes = kNoAllocScratchBytes;
+    }
     if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255u)) {
         return fail(CLK_INTERNAL, "volta_mma_bwd: the workspace must be 256-byte aligned and hold " +
                                       std::to_string(need) + " bytes");
@@ -1170,5 +1219,19 @@ extern "C" int clk_attention_bwd(clk_stream stream, int32_t device, const clk_bu
                                  const clk_buffer* dbias, float scale, int32_t want_dbias,
                                  void* workspace, size_t workspace_bytes) {
     return attention_bwd_impl(stream, device, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
-                              dbias, scale, want_dbias, workspace, workspace_bytes);
+                              dbias, scale, want_dbias, workspace, workspace_bytes, false);
 }
+
+extern "C" int clk_attention_bwd_noalloc(clk_stream stream, int32_t device, const clk_buffer* q,
+                                         const clk_buffer* k, const clk_buffer* v,
+                                         const clk_buffer* bias, const clk_buffer* kmask,
+                                         const clk_buffer* out, const clk_buffer* dout,
+                                         const clk_buffer* lse, const clk_buffer* dq,
+                                         const clk_buffer* dk, const clk_buffer* dv,
+                                         const clk_buffer* dbias, float scale,
+                                         int32_t want_dbias) {
+    return attention_bwd_impl(stream, device, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
+                              dbias, scale, want_dbias, nullptr, 0, true);
+}
+
+extern "C" size_t clk_attention_bwd_noalloc_scratch_size(void) { return kNoAllocScratchBytes; }

@@ -93,6 +93,24 @@ int clk_attention_bwd(clk_stream stream, int32_t device, const clk_buffer* q, co
  * backward would reject; the call itself then reports why). */
 size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buffer* q, const clk_buffer* k);
 
+/* No counterpart in the reference: clk_attention_bwd for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same buffers, flags,
+ * validation and results (bit-identical), but no workspace argument: the scratch is a static
+ * device array of the library, one per GPU, of clk_attention_bwd_noalloc_scratch_size() bytes
+ * (96 MiB, enough for [512, 8, 384, 32]), held until the process ends. Shapes whose scratch
+ * would exceed it are rejected with CLK_INVALID_ARGUMENT before any launch. The call allocates
+ * nothing. Every call on a GPU shares that GPU's scratch, so calls that overlap on one GPU (two
+ * streams, or two threads) race and must be serialised by the caller. */
+int clk_attention_bwd_noalloc(clk_stream stream, int32_t device, const clk_buffer* q,
+                              const clk_buffer* k, const clk_buffer* v, const clk_buffer* bias,
+                              const clk_buffer* kmask, const clk_buffer* out,
+                              const clk_buffer* dout, const clk_buffer* lse, const clk_buffer* dq,
+                              const clk_buffer* dk, const clk_buffer* dv, const clk_buffer* dbias,
+                              float scale, int32_t want_dbias);
+
+/* Bytes of the static scratch behind clk_attention_bwd_noalloc. */
+size_t clk_attention_bwd_noalloc_scratch_size(void);
+
 /* Diagnostic, no counterpart in the reference: the backward's launch plan for these shapes on
  * this device, plan[0..count) = {row groups per dK/dV workgroup, batch rows per workgroup
  * (chunk), chunks, row passes per workgroup, query windows}. */
