@@ -69,8 +69,12 @@ def build(jobs=None, verbose=False):
         objs = list(ex.map(lambda s: compile_one(cc, s, verbose), srcs))
     lib = os.path.join(OUT_DIR, LIB_NAME)
     tmp = lib + ".tmp"
+    # libstdc++ and libgcc are linked statically, as the reference links its libraries
+    # (its CI audits for them): the library then needs the HIP runtime and the C library only,
+    # whatever C++ runtime the host process (jaxlib, torch) brings
     cmd = [cc, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + objs + \
-          ["-Wl,--no-undefined", "-Wl,-soname," + LIB_NAME]
+          ["-static-libstdc++", "-static-libgcc", "-Wl,--no-undefined", "-Wl,-soname," + LIB_NAME,
+           "-Wl,--exclude-libs,ALL", "-Wl,--version-script=" + os.path.join(HERE, "exports.map")]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
