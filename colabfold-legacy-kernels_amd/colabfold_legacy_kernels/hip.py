@@ -14,7 +14,9 @@ stream, with the FFI binding's buffer order, attributes, result shapes and error
   gated_dual_proj     VoltaGdp            (volta_ops.cu:258-269)
 
 Results are allocated here with torch (as XLA preallocates them) unless passed in, which is how a
-caller aliases an output to its residual / input. A rejected call raises InvalidArgument (the
+caller aliases an output to its residual / input. The fused ops take fp16 or bf16 activations
+(all of a call's activations and results one type; weights, biases and keep fp16); results come
+back in the activation type. A rejected call raises InvalidArgument (the
 FFI's InvalidArgument) and a launch failure KernelError (Internal), with the library's message.
 There is no CPU fallback: without the built library every call raises.
 """
@@ -24,9 +26,9 @@ import torch
 
 from . import library_path
 
-CLK_S32, CLK_U8, CLK_F16, CLK_F32 = 4, 6, 10, 11
+CLK_S32, CLK_U8, CLK_F16, CLK_F32, CLK_BF16 = 4, 6, 10, 11, 16
 _DTYPES = {torch.int32: CLK_S32, torch.uint8: CLK_U8, torch.float16: CLK_F16,
-           torch.float32: CLK_F32}
+           torch.float32: CLK_F32, torch.bfloat16: CLK_BF16}
 INVALID_ARGUMENT, INTERNAL = 3, 13
 
 
@@ -209,8 +211,8 @@ def attention_bwd_noalloc(q, k, v, bias, kmask, out, dout, lse, scale, want_dbia
 def ln_gdp(x, scale, offset, wpT, bp, wgT, bg, mask, eps=1e-5):
     """VoltaLnGdp: left, right [P/2, M] F16, channel major."""
     m, p = x.shape[0], wpT.shape[0]
-    left = torch.empty((p // 2, m), dtype=torch.float16, device=x.device)
-    right = torch.empty((p // 2, m), dtype=torch.float16, device=x.device)
+    left = torch.empty((p // 2, m), dtype=x.dtype, device=x.device)
+    right = torch.empty((p // 2, m), dtype=x.dtype, device=x.device)
     bufs = [buffer(t) for t in (x, scale, offset, wpT, bp, wgT, bg, mask, left, right)]
     _check(lib().clk_ln_gdp(_stream(x), *map(_ref, bufs), float(eps)))
     return left, right
@@ -220,7 +222,7 @@ def trimul_epilogue(x_cm, x, in_scale, in_offset, ln_scale, ln_offset, woT, bo, 
                     keep=None, eps=1e-5, add_input=False, out=None):
     """VoltaTrimulEpilogue: out [M,O] F16. out may be x itself with add_input."""
     m, o = x.shape[0], woT.shape[0]
-    out = torch.empty((m, o), dtype=torch.float16, device=x.device) if out is None else out
+    out = torch.empty((m, o), dtype=x.dtype, device=x.device) if out is None else out
     has_keep = keep is not None
     keep = keep if has_keep else _one(x, torch.float16)
     bufs = [buffer(t) for t in (x_cm, x, in_scale, in_offset, ln_scale, ln_offset, woT, bo, wgT,
@@ -236,9 +238,9 @@ def ln_projection(x, scale, offset, wT=None, wbT=None, keep=None, eps=1e-5):
     m = x.shape[0]
     n = 0 if wT is None else wT.shape[0]
     heads = 0 if wbT is None else wbT.shape[0]
-    p = torch.empty((m, n), dtype=torch.float16, device=x.device) if n else _one(x, torch.float16)
-    bias = (torch.empty((heads, m), dtype=torch.float16, device=x.device) if heads
-            else _one(x, torch.float16))
+    p = torch.empty((m, n), dtype=x.dtype, device=x.device) if n else _one(x, x.dtype)
+    bias = (torch.empty((heads, m), dtype=x.dtype, device=x.device) if heads
+            else _one(x, x.dtype))
     has_keep = keep is not None
     keep = keep if has_keep else _one(x, torch.float16)
     wT = wT if n else _one(x, torch.float16)
@@ -252,9 +254,9 @@ def ln_projection(x, scale, offset, wT=None, wbT=None, keep=None, eps=1e-5):
 def output_projection(o, wT, b, residual=None, keep=None, out=None):
     """VoltaOutProj: out [M,N] = o@w + b [+ residual]; out may be residual itself."""
     m, n = o.shape[0], wT.shape[0]
-    out = torch.empty((m, n), dtype=torch.float16, device=o.device) if out is None else out
+    out = torch.empty((m, n), dtype=o.dtype, device=o.device) if out is None else out
     has_residual = residual is not None
-    residual = residual if has_residual else _one(o, torch.float16)
+    residual = residual if has_residual else _one(o, o.dtype)
     has_keep = keep is not None
     keep = keep if has_keep else _one(o, torch.float16)
     bufs = [buffer(t) for t in (o, wT, b, residual, keep, out)]

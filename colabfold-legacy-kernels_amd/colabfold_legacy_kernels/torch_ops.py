@@ -20,7 +20,8 @@ provides on top of `hip` (the C ABI binding):
                    other widths and dtypes decline to the caller's own path)
 
 Everything runs on the GPU through the built library; there is no CPU path. The fused wrappers
-are forward only (the reference's callers take their gradients from jnp references).
+are forward only (the reference's callers take their gradients from jnp references). They take
+fp16 or bf16 activations, with weights and biases cast to fp16 for the kernels.
 """
 import torch
 
@@ -101,10 +102,11 @@ def trim_limits(kmask):
 # ---- fused pair-stack ops with natural weight shapes ----------------------------------------
 
 def fused_available(kernel, dtype, *widths):
-    """True if `kernel` takes these widths and this activation dtype (fp16 only, as the
-    reference's FFI binds F16): ln_gated_dual_proj (a, ci), trimul_epilogue (a, ci),
-    ln_projection (a, n), output_projection (k, c), transition (c, hidden)."""
-    if dtype != torch.float16:
+    """True if `kernel` takes these widths and this activation dtype: ln_gated_dual_proj (a, ci),
+    trimul_epilogue (a, ci), ln_projection (a, n), output_projection (k, c), transition (c,
+    hidden). fp16 is the reference's F16 contract; bf16 activations are this library's addition
+    (the reference's wrappers decline them, tests/test_fused.py:223-229)."""
+    if dtype not in (torch.float16, torch.bfloat16):
         return False
     w2 = {64, 128}
     if kernel in ("ln_gated_dual_proj", "trimul_epilogue"):
@@ -132,13 +134,18 @@ def _keep_rows(keep):
     return None if keep is None else keep.reshape(-1).to(torch.float16).contiguous()
 
 
+def _w16(w):
+    """Weights and biases go to the kernels as fp16."""
+    return w.to(torch.float16)
+
+
 def ln_gated_dual_proj(x, scale, offset, wp, bp, wg, bg, mask, eps=1e-5):
     """left, right [ci, M] (channel major) = the halves of mask (LN(x)@wp + bp) sigmoid(LN(x)@wg
     + bg), with wp, wg [a, 2 ci] (tests/test_fused.py:96-103)."""
     x2, _ = _rows(x)
-    wpT, wgT = layouts.proj_pair_T(wp, wg)
+    wpT, wgT = layouts.proj_pair_T(_w16(wp), _w16(wg))
     return hip.ln_gdp(x2, scale.float().contiguous(), offset.float().contiguous(), wpT,
-                      bp.contiguous(), wgT, bg.contiguous(), _keep_rows(mask), eps)
+                      _w16(bp).contiguous(), wgT, _w16(bg).contiguous(), _keep_rows(mask), eps)
 
 
 def trimul_epilogue_ln(x_cm, x, in_scale, in_offset, ln_scale, ln_offset, wo, bo, wg, bg,
@@ -149,8 +156,9 @@ def trimul_epilogue_ln(x_cm, x, in_scale, in_offset, ln_scale, ln_offset, wo, bo
     x2, lead = _rows(x)
     out = hip.trimul_epilogue(x_cm.float().contiguous(), x2, in_scale.float().contiguous(),
                               in_offset.float().contiguous(), ln_scale.float().contiguous(),
-                              ln_offset.float().contiguous(), layouts.linear_T(wo), bo.contiguous(),
-                              layouts.linear_T(wg), bg.contiguous(), keep=_keep_rows(keep), eps=eps,
+                              ln_offset.float().contiguous(), layouts.linear_T(_w16(wo)),
+                              _w16(bo).contiguous(), layouts.linear_T(_w16(wg)),
+                              _w16(bg).contiguous(), keep=_keep_rows(keep), eps=eps,
                               add_input=add_input, out=x2 if add_input else None)
     return out.reshape(lead + (out.shape[-1],))
 
@@ -160,8 +168,8 @@ def ln_projection(x, scale, offset, w=None, wb=None, keep=None, eps=1e-5):
     [heads, ...] = (LN(x)@wb)^T, with w [slots, a, n] and wb [a, heads]; either may be None
     (tests/test_fused.py:180-199)."""
     x2, lead = _rows(x)
-    wT = None if w is None else layouts.slot_major(w)
-    wbT = None if wb is None else layouts.heads_T(wb)
+    wT = None if w is None else layouts.slot_major(_w16(w))
+    wbT = None if wb is None else layouts.heads_T(_w16(wb))
     p, b = hip.ln_projection(x2, scale.float().contiguous(), offset.float().contiguous(), wT, wbT,
                              keep=_keep_rows(keep), eps=eps)
     if p is not None:
@@ -176,7 +184,7 @@ def output_projection(o, w, b, residual=None, keep=None):
     it, as the target aliases them (tests/test_fused.py:201-213)."""
     o2, lead = _rows(o)
     r2 = None if residual is None else residual.reshape(-1, residual.shape[-1]).contiguous()
-    out = hip.output_projection(o2, layouts.linear_T(w), b.contiguous(), residual=r2,
+    out = hip.output_projection(o2, layouts.linear_T(_w16(w)), _w16(b).contiguous(), residual=r2,
                                 keep=_keep_rows(keep), out=r2)
     return out.reshape(lead + (out.shape[-1],))
 
@@ -186,7 +194,8 @@ def transition(x, scale, offset, w1, b1, w2, b2, keep=None, add_input=False, eps
     (tests/test_fused.py:215-229); with add_input the result is written over x."""
     x2, lead = _rows(x)
     out = hip.transition(x2, scale.float().contiguous(), offset.float().contiguous(),
-                         layouts.linear_T(w1), b1.contiguous(), layouts.w2_blocked(w2),
-                         b2.contiguous(), keep=_keep_rows(keep), eps=eps, add_input=add_input,
+                         layouts.linear_T(_w16(w1)), _w16(b1).contiguous(),
+                         layouts.w2_blocked(_w16(w2)), _w16(b2).contiguous(),
+                         keep=_keep_rows(keep), eps=eps, add_input=add_input,
                          out=x2 if add_input else None)
     return out.reshape(lead + (out.shape[-1],))

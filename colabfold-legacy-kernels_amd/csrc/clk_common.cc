@@ -19,6 +19,7 @@ const char* type_name(int t) {
     case CLK_U8: return "U8";
     case CLK_F16: return "F16";
     case CLK_F32: return "F32";
+    case CLK_BF16: return "BF16";
     default: return "?";
     }
 }

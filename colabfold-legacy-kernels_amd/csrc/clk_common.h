@@ -35,6 +35,31 @@ __device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Activations of the fused ops are fp16 (the reference's F16 contract) or bf16 (BF). Loads keep
+// the raw 16-bit patterns in half8 registers and convert where the value is used; a bf16 value
+// converts to fp16 exactly within fp16's normal range, so MFMA operands stay fp16. Results are
+// rounded to the activation type once, on store (v_cvt_pk_bf16_f32 for bf16).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <bool BF>
+__device__ __forceinline__ float act_get(half8 raw, int e) {
+    if constexpr (BF) {
+        return (float)__builtin_bit_cast(bf16x8, raw)[e];
+    } else {
+        return (float)raw[e];
+    }
+}
+
+// v rounded to the activation type, as a raw 16-bit pattern
+template <bool BF>
+__device__ __forceinline__ half_t act_cvt(float v) {
+    if constexpr (BF) {
+        return __builtin_bit_cast(half_t, (__bf16)v);
+    } else {
+        return (half_t)v;
+    }
+}
+
 // LDS row of tile row x, for operand tiles whose A row r of block b is
 //   x = per (r / 4) + 4 b + r % 4:
 // stored at row 16 b + r, a 16-lane group reads 16 consecutive rows, which with a row stride of

@@ -126,7 +126,7 @@ __device__ __forceinline__ float group_sum(float s) {
     return s;
 }
 
-template <int K, int R, bool QUAD, bool LN, int TH>
+template <int K, int R, bool QUAD, bool LN, int TH, bool BF = false>
 __device__ __forceinline__ void ln_rows_to_frags(half_t* Xf, const RowTile<K, R, TH>& t,
                                                  const float* sc, const float* of, float eps) {
     using RT = RowTile<K, R, TH>;
@@ -138,14 +138,14 @@ __device__ __forceinline__ void ln_rows_to_frags(half_t* Xf, const RowTile<K, R,
 #pragma unroll
         for (int j = 0; j < RT::kChunks; ++j)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s += (float)t.v[j][e];
+            for (int e = 0; e < 8; ++e) s += act_get<BF>(t.v[j], e);
         mean = group_sum<TPR>(s) * (1.f / K);
         float q = 0.f;
 #pragma unroll
         for (int j = 0; j < RT::kChunks; ++j)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float d = (float)t.v[j][e] - mean;
+                const float d = act_get<BF>(t.v[j], e) - mean;
                 q += d * d;
             }
         rstd = __builtin_amdgcn_rsqf(group_sum<TPR>(q) * (1.f / K) + eps);
@@ -168,8 +168,12 @@ __device__ __forceinline__ void ln_rows_to_frags(half_t* Xf, const RowTile<K, R,
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const int col = 8 * c + e;
-                y[e] = (half_t)(((float)t.v[j][e] - mean) * rstd * sc[col] + of[col]);
+                y[e] = (half_t)((act_get<BF>(t.v[j], e) - mean) * rstd * sc[col] + of[col]);
             }
+        } else if constexpr (BF) {
+            // bf16 to fp16: exact within fp16's normal range
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = (half_t)act_get<true>(t.v[j], e);
         } else {
             y = t.v[j];
         }
@@ -198,7 +202,7 @@ struct ProjArgs {
 // TH threads share the LDS-resident weights. The 64 x ncols output tile is split into items of
 // one column pair (32 outputs) and 4 / split row blocks: with at least as many pairs as waves a
 // wave takes whole pairs, otherwise `split` waves share a pair and divide its four row blocks.
-template <int K, bool LN, int TH>
+template <int K, bool LN, int TH, bool BF>
 __global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
     constexpr int KS = K / 32, TW = TH / kWave;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
             continue;
         }
         __syncthreads();  // the previous tile's operand reads are done
-        ln_rows_to_frags<K, kTileRows, false, LN>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<K, kTileRows, false, LN, TH, BF>(Xf, xt, sc, of, a.eps);
         __syncthreads();
         if (tile + gridDim.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, (tile + gridDim.x) * kTileRows);
 
@@ -300,14 +304,14 @@ __global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
                 half8 o;
                 if constexpr (LN) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = (half_t)acc[j >> 2][rb][j & 3];
+                    for (int j = 0; j < 8; ++j) o[j] = act_cvt<BF>(acc[j >> 2][rb][j & 3]);
                 } else if (a.residual != nullptr) {
                     const half8 res = fld8(a.residual + (int64_t)row * a.n + col);
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[j] + (float)res[j]);
+                    for (int j = 0; j < 8; ++j) o[j] = act_cvt<BF>(acc[j >> 2][rb][j & 3] + bv[j] + act_get<BF>(res, j));
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[j]);
+                    for (int j = 0; j < 8; ++j) o[j] = act_cvt<BF>(acc[j >> 2][rb][j & 3] + bv[j]);
                 }
                 fst8(dst, o);
             }
@@ -334,7 +338,7 @@ __global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int h = 4 * g + i;
-                    if (h < a.heads && row < a.M) a.bias[(int64_t)h * a.M + row] = (half_t)acc[rb][i];
+                    if (h < a.heads && row < a.M) a.bias[(int64_t)h * a.M + row] = act_cvt<BF>(acc[rb][i]);
                 }
             }
         }
@@ -348,7 +352,7 @@ __global__ __launch_bounds__(TH) void proj_kernel(ProjArgs a) {
 // covers only them, not the stores issued after them. The partial last tile, if any, follows the
 // loop with per-row checks.
 // At K = 64 two workgroups share a CU (LDS allows it), so the kernel is held to 128 VGPRs.
-template <int K, bool LN, int TH, int PAIRS>
+template <int K, bool LN, int TH, int PAIRS, bool BF>
 __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs a) {
     constexpr int KS = K / 32, TW = TH / kWave, NP = PAIRS * TW;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
                 }
         }
         __syncthreads();  // the previous tile's operand reads are done
-        ln_rows_to_frags<K, kTileRows, false, LN>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<K, kTileRows, false, LN, TH, BF>(Xf, xt, sc, of, a.eps);
         __syncthreads();
         fetch(min(tile + (int)gridDim.x, tiles - 1));
 
@@ -447,14 +451,14 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
                 half8 o;
                 if constexpr (LN) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = (half_t)acc[j >> 2][rb][j & 3];
+                    for (int j = 0; j < 8; ++j) o[j] = act_cvt<BF>(acc[j >> 2][rb][j & 3]);
                 } else if (a.residual != nullptr) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[pp][j] + (float)res[pp][rb][j]);
+                        o[j] = act_cvt<BF>(acc[j >> 2][rb][j & 3] + bv[pp][j] + act_get<BF>(res[pp][rb], j));
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) o[j] = (half_t)(acc[j >> 2][rb][j & 3] + bv[pp][j]);
+                    for (int j = 0; j < 8; ++j) o[j] = act_cvt<BF>(acc[j >> 2][rb][j & 3] + bv[pp][j]);
                 }
                 if constexpr (K == 128) {
                     fst8_nt(a.out + (int64_t)row * a.n + col, o);
@@ -480,7 +484,7 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int h = 4 * g + i;
-                    if (h < a.heads && (kFull || row < a.M)) a.bias[(int64_t)h * a.M + row] = (half_t)acc[rb][i];
+                    if (h < a.heads && (kFull || row < a.M)) a.bias[(int64_t)h * a.M + row] = act_cvt<BF>(acc[rb][i]);
                 }
             }
         }
@@ -518,7 +522,7 @@ __global__ __launch_bounds__(TH, K == 64 ? 4 : 1) void proj_fast_kernel(ProjArgs
 // same iteration after them; the keep decision from a ballot of the tile's 64 rows; dropped
 // buffer stores for skipped tiles, for padding that must keep the residual the output aliases,
 // and for rows past M.
-template <int K, int N, bool RES>
+template <int K, int N, bool RES, bool BF>
 __global__ __launch_bounds__(kProjThreads, 4) void outproj_kernel(ProjArgs a) {
     constexpr int TH = kProjThreads, KS = K / 32, TW = TH / kWave;
     constexpr int NPAIRS = N / 32, SPLIT = TW / NPAIRS, RBW = 4 / SPLIT;
@@ -576,11 +580,11 @@ __global__ __launch_bounds__(kProjThreads, 4) void outproj_kernel(ProjArgs a) {
         const uint64_t live = __ballot(k > 0.f), zero = __ballot(k == 0.f);
         work = live ? (int)kCompute : zero ? (int)kPadding : (int)kSkip;
         __syncthreads();  // the previous tile's operand reads are done
-        ln_rows_to_frags<K, kTileRows, false, false>(Xf, xt, nullptr, nullptr, 0.f);
+        ln_rows_to_frags<K, kTileRows, false, false, TH, BF>(Xf, xt, nullptr, nullptr, 0.f);
 #pragma unroll
         for (int i = 0; i < RBW; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) resf[i][j] = RES ? pin_f32((float)rs[i][j]) : 0.f;  // here, not after the next fetch
+            for (int j = 0; j < 8; ++j) resf[i][j] = RES ? pin_f32(act_get<BF>(rs[i], j)) : 0.f;  // here, not after the next fetch
         __syncthreads();
     };
     const auto gemm_store = [&](int t) {
@@ -612,7 +616,7 @@ __global__ __launch_bounds__(kProjThreads, 4) void outproj_kernel(ProjArgs a) {
             half8 o;
 #pragma unroll
             for (int j = 0; j < 8; ++j)
-                o[j] = (half_t)(work == kPadding ? 0.f : acc[j >> 2][i][j & 3] + bv[j] + resf[i][j]);
+                o[j] = act_cvt<BF>(work == kPadding ? 0.f : acc[j >> 2][i][j & 3] + bv[j] + resf[i][j]);
             const uint32_t off = (uint32_t)((16 * (rb0 + i) + r16) * N + col) * 2u;
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
         }
@@ -641,7 +645,7 @@ __global__ __launch_bounds__(kProjThreads, 4) void outproj_kernel(ProjArgs a) {
 // one or two contiguous rows (1 KB). The loop is rotated like the other straight-line kernels:
 // the next tile's rows are fetched before this tile's products and stores and normalised after
 // them. The head-bias block (channel-major) is computed and stored by the last wave as before.
-template <int K, int N>
+template <int K, int N, bool BF>
 __global__ __launch_bounds__(kProjThreads, K == 64 ? 4 : 2) void proj_rows_kernel(ProjArgs a) {
     constexpr int TH = kProjThreads, KS = K / 32, TW = TH / kWave, PAIRS = N / 32 / TW;
     constexpr int RCH = N / 8;                   // 16-byte chunks of an output row
@@ -691,7 +695,7 @@ __global__ __launch_bounds__(kProjThreads, K == 64 ? 4 : 2) void proj_rows_kerne
     };
     const auto prepare = [&]() {
         __syncthreads();  // the previous tile's operand reads and output-tile reads are done
-        ln_rows_to_frags<K, kTileRows, false, true>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<K, kTileRows, false, true, TH, BF>(Xf, xt, sc, of, a.eps);
         __syncthreads();
     };
     const auto compute_store = [&](int t) {
@@ -711,7 +715,7 @@ __global__ __launch_bounds__(kProjThreads, K == 64 ? 4 : 2) void proj_rows_kerne
                     for (int hb = 0; hb < 2; ++hb) acc[hb] = mfma16x16x32(wa[pp][hb][ks], xop[ks], acc[hb]);
                 half8 o;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = (half_t)acc[j >> 2][j & 3];
+                for (int j = 0; j < 8; ++j) o[j] = act_cvt<BF>(acc[j >> 2][j & 3]);
                 const int chunk = 4 * (wave + pp * TW) + g;
                 fst8(Ot + row * N + 8 * (chunk ^ (row & 15)), o);
             }
@@ -723,7 +727,7 @@ __global__ __launch_bounds__(kProjThreads, K == 64 ? 4 : 2) void proj_rows_kerne
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int h = 4 * g + i;
-                    if (h < a.heads && m < a.M) a.bias[(int64_t)h * a.M + m] = (half_t)hacc[i];
+                    if (h < a.heads && m < a.M) a.bias[(int64_t)h * a.M + m] = act_cvt<BF>(hacc[i]);
                 }
             }
         }
@@ -770,7 +774,7 @@ struct LnGdpArgs {
     float eps;
 };
 
-template <int K, int TH>
+template <int K, int TH, bool BF>
 __global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
     constexpr int KS = K / 32, TW = TH / kWave;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
@@ -812,7 +816,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
             continue;
         }
         __syncthreads();
-        ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<K, kTileRows, true, true, TH, BF>(Xf, xt, sc, of, a.eps);
         __syncthreads();
         if (tile + gridDim.x < tiles) fetch_rows<K, kTileRows>(xt, a.x, a.M, (tile + gridDim.x) * kTileRows);
 
@@ -856,7 +860,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
                 for (int i = 0; i < 4; ++i) {
                     const int t = 4 * rb + i;
                     const float v = mv[t] * (ap[rb][i] + bpv) * sigmoid_fast(ag[rb][i] + bgv);
-                    if (t < 8) lo[t] = (half_t)v; else hi[t - 8] = (half_t)v;
+                    if (t < 8) lo[t] = act_cvt<BF>(v); else hi[t - 8] = act_cvt<BF>(v);
                 }
             const int rows_left = a.M - (m0 + 16 * g);
             if (vec && rows_left >= 16) {
@@ -884,7 +888,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_kernel(LnGdpArgs a) {
 //   the hardware drops, so every tile issues the same stores and no branch skips them;
 // - each wave owns CBW column blocks, fixed at compile time, with their biases in registers.
 // Offsets are 32-bit: the launcher requires P/2 * M * 2 bytes < 2^31.
-template <int K, int PH, int TH>
+template <int K, int PH, int TH, bool BF>
 __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
     constexpr int KS = K / 32, TW = TH / kWave, NB = PH / 8, CBW = NB / TW;
     static_assert(NB % TW == 0, "whole column blocks per wave");
@@ -986,7 +990,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
                     const int e = 4 * rb + i;
                     float v = mv[e] * (ap[rb][i] + bpv[j]) * sigmoid_fast(ag[rb][i] + bgv[j]);
                     v = zero_out ? 0.f : v;
-                    if (e < 8) lo[e] = (half_t)v; else hi[e - 8] = (half_t)v;
+                    if (e < 8) lo[e] = act_cvt<BF>(v); else hi[e - 8] = act_cvt<BF>(v);
                 }
             // column block cb lies wholly in left (columns < PH) or in right
             const int col = 16 * cb + r16;
@@ -1004,7 +1008,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
     fetch(t);
     int work = decide(t);
     __syncthreads();  // the weights and LayerNorm parameters are in LDS (decide has no barrier)
-    ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
+    ln_rows_to_frags<K, kTileRows, true, true, TH, BF>(Xf, xt, sc, of, a.eps);
     __syncthreads();
     for (;;) {
         const int nt = t + G;
@@ -1014,7 +1018,7 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
         t = nt;
         work = decide(t);
         __syncthreads();  // every wave has read the previous tile's operands
-        ln_rows_to_frags<K, kTileRows, true, true>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<K, kTileRows, true, true, TH, BF>(Xf, xt, sc, of, a.eps);
         __syncthreads();
     }
 }
@@ -1056,7 +1060,7 @@ constexpr int epi_waves(int C, int CA, int O, bool ADD) {
 // - every tile runs both LayerNorms and the GEMMs; padding stores zeros, and the stores of skipped
 //   rows and rows past M are buffer stores at an offset past the tile's end, which the hardware
 //   drops, so no branch skips them.
-template <int C, int CA, int O, bool ADD>
+template <int C, int CA, int O, bool ADD, bool BF>
 __global__ __launch_bounds__(kEpiThreads, epi_waves(C, CA, O, ADD))
 void epilogue_kernel(EpiArgs a) {
     constexpr int TH = kEpiThreads, KC = C / 32, KA = CA / 32, TW = TH / kWave;
@@ -1178,11 +1182,11 @@ void epilogue_kernel(EpiArgs a) {
             const int c = (cq * CQ + i) / 8;
             fst8(Yf + frag(r >> 4, c >> 2, KC, (r & 15) + 16 * (c & 3)), y);
         }
-        ln_rows_to_frags<CA, kTileRows, false, true>(Af, xt, isc, iof, a.eps);
+        ln_rows_to_frags<CA, kTileRows, false, true, TH, BF>(Af, xt, isc, iof, a.eps);
 #pragma unroll
         for (int i = 0; i < RBW; ++i)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) res[i][j] = ADD ? pin_f32((float)xa[i][j]) : 0.f;  // here, not after the next fetch
+            for (int j = 0; j < 8; ++j) res[i][j] = ADD ? pin_f32(act_get<BF>(xa[i], j)) : 0.f;  // here, not after the next fetch
         __syncthreads();
     };
     const auto gemm_store = [&](int t) {
@@ -1227,7 +1231,7 @@ void epilogue_kernel(EpiArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float val = (ao[j >> 2][i][j & 3] + bov[j]) * sigmoid_fast(ag[j >> 2][i][j & 3] + bgv[j]);
-                o[j] = (half_t)(w == kPadding ? 0.f : val + res[i][j]);
+                o[j] = act_cvt<BF>(w == kPadding ? 0.f : val + res[i][j]);
             }
             const uint32_t off = (uint32_t)((16 * rb + r16) * O + col) * 2u;
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
@@ -1288,7 +1292,7 @@ struct TransTile {
 constexpr int trans_threads(int C) { return C <= 128 ? 512 : 256; }
 constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
 
-template <int C, bool ADD, int TH>
+template <int C, bool ADD, int TH, bool BF>
 __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_kernel(TransArgs a) {
     using T = TransTile<C>;
     constexpr int TW = TH / kWave, RB = kTransRows / 16 / TW, kCPT = T::kChunks / TH;
@@ -1365,7 +1369,7 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
         }
         if (!PF) fetch_rows<C, kTransRows>(xt, a.x, a.M, m0);
         __syncthreads();
-        ln_rows_to_frags<C, kTransRows, false, true>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<C, kTransRows, false, true, TH, BF>(Xf, xt, sc, of, a.eps);
 
         float4v acc[NCB][RB];
 #pragma unroll
@@ -1445,7 +1449,7 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
                 half8 o;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    o[e] = (half_t)(acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + (float)xa[e]);
+                    o[e] = act_cvt<BF>(acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + act_get<BF>(xa, e));
                 fst8(dst, o);
             }
         }
@@ -1510,12 +1514,59 @@ using namespace clk;
 static const half_t* f16p(const clk_buffer* b) { return static_cast<const half_t*>(b->data); }
 static const float* f32p(const clk_buffer* b) { return static_cast<const float*>(b->data); }
 
+template <bool BF>
+static int ln_gdp_launch(const LnGdpArgs& a, int64_t M, int64_t K, int64_t P, hipStream_t s) {
+    const size_t lds = (size_t)(2 * P * K + kTileRows * K) * 2 + 2 * K * 4;
+    const int64_t tiles = (M + kTileRows - 1) / kTileRows;
+    const dim3 grid(persistent_grid(tiles, lds));
+    if (M % 8 == 0 && P / 2 * M * 2 < (int64_t{1} << 31)) {  // 16-byte channel-major stores, 32-bit offsets
+#define CLK_GDP_FAST(K_, PH_)                                                                          \
+    if (K == K_ && P / 2 == PH_) {                                                                     \
+        const auto kern = ln_gdp_fast_kernel<K_, PH_, gdp_threads<K_>(), BF>;                          \
+        if (int st = launch_fused("ln_gdp", kern, grid, lds, s, &a, 0)) return st;                     \
+        stage_mark(s, 0);                                                                              \
+        hipLaunchKernelGGL(kern, grid, dim3(gdp_threads<K_>()), lds, s, a);                            \
+        stage_mark(s, 1);                                                                              \
+        return launch_status("ln_gdp");                                                                \
+    }
+        CLK_GDP_FAST(64, 64) CLK_GDP_FAST(64, 128) CLK_GDP_FAST(128, 64) CLK_GDP_FAST(128, 128)
+#undef CLK_GDP_FAST
+    }
+    if (K == 64) {
+        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64, gdp_threads<64>(), BF>, grid, lds, s, &a, 0)) return st;
+        stage_mark(s, 0);
+        hipLaunchKernelGGL((ln_gdp_kernel<64, gdp_threads<64>(), BF>), grid, dim3(gdp_threads<64>()), lds, s, a);
+        stage_mark(s, 1);
+    } else {
+        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<128, gdp_threads<128>(), BF>, grid, lds, s, &a, 0)) return st;
+        stage_mark(s, 0);
+        hipLaunchKernelGGL((ln_gdp_kernel<128, gdp_threads<128>(), BF>), grid, dim3(gdp_threads<128>()), lds, s, a);
+        stage_mark(s, 1);
+    }
+    return launch_status("ln_gdp");
+}
+
+// The activation type of a fused call: fp16 (the reference's contract) or bf16, one for all of
+// the call's activation buffers (`acts`); CLK_F16 if the first is neither, so the type check
+// reports it.
+static int act_type(const clk_buffer* first) {
+    return first != nullptr && first->dtype == CLK_BF16 ? CLK_BF16 : CLK_F16;
+}
+
+// The type an optional activation buffer must have: the call's activation type when it is used;
+// an unused one-element stand-in may be F16 or BF16.
+static int opt_act_type(const clk_buffer* b, bool used, int at) {
+    if (used || b == nullptr) return at;
+    return b->dtype == CLK_F16 || b->dtype == CLK_BF16 ? b->dtype : at;
+}
+
 extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
                           const clk_buffer* offset, const clk_buffer* wpT, const clk_buffer* bp,
                           const clk_buffer* wgT, const clk_buffer* bg, const clk_buffer* mask,
                           const clk_buffer* left, const clk_buffer* right, float eps) {
     const clk_buffer* bufs[] = {x, scale, offset, wpT, bp, wgT, bg, mask, left, right};
-    const int types[] = {CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    const int at = act_type(x);
+    const int types[] = {at, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, at, at};
     if (int st = check_types("ln_gdp", bufs, types, 10)) return st;
     if (x->rank != 2 || wpT->rank != 2 || wpT->dims[1] != x->dims[1]) {
         return invalid("ln_gdp: x must be [M,K] and wpT [P,K]");
@@ -1534,60 +1585,33 @@ extern "C" int clk_ln_gdp(clk_stream stream, const clk_buffer* x, const clk_buff
     }
     LnGdpArgs a{f16p(x), f32p(scale), f32p(offset), f16p(wpT), f16p(bp), f16p(wgT), f16p(bg), f16p(mask),
                 static_cast<half_t*>(left->data), static_cast<half_t*>(right->data), (int)M, (int)P, eps};
-    const size_t lds = (size_t)(2 * P * K + kTileRows * K) * 2 + 2 * K * 4;
-    const int64_t tiles = (M + kTileRows - 1) / kTileRows;
-    const dim3 grid(persistent_grid(tiles, lds));
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (M % 8 == 0 && P / 2 * M * 2 < (int64_t{1} << 31)) {  // 16-byte channel-major stores, 32-bit offsets
-#define CLK_GDP_FAST(K_, PH_)                                                                          \
-    if (K == K_ && P / 2 == PH_) {                                                                     \
-        const auto kern = ln_gdp_fast_kernel<K_, PH_, gdp_threads<K_>()>;                              \
-        if (int st = launch_fused("ln_gdp", kern, grid, lds, s, &a, 0)) return st;                     \
-        stage_mark(s, 0);                                                                              \
-        hipLaunchKernelGGL(kern, grid, dim3(gdp_threads<K_>()), lds, s, a);                            \
-        stage_mark(s, 1);                                                                              \
-        return launch_status("ln_gdp");                                                                \
-    }
-        CLK_GDP_FAST(64, 64) CLK_GDP_FAST(64, 128) CLK_GDP_FAST(128, 64) CLK_GDP_FAST(128, 128)
-#undef CLK_GDP_FAST
-    }
-    if (K == 64) {
-        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<64, gdp_threads<64>()>, grid, lds, s, &a, 0)) return st;
-        stage_mark(s, 0);
-        hipLaunchKernelGGL((ln_gdp_kernel<64, gdp_threads<64>()>), grid, dim3(gdp_threads<64>()), lds, s, a);
-        stage_mark(s, 1);
-    } else {
-        if (int st = launch_fused("ln_gdp", ln_gdp_kernel<128, gdp_threads<128>()>, grid, lds, s, &a, 0)) return st;
-        stage_mark(s, 0);
-        hipLaunchKernelGGL((ln_gdp_kernel<128, gdp_threads<128>()>), grid, dim3(gdp_threads<128>()), lds, s, a);
-        stage_mark(s, 1);
-    }
-    return launch_status("ln_gdp");
+    return at == CLK_BF16 ? ln_gdp_launch<true>(a, M, K, P, s) : ln_gdp_launch<false>(a, M, K, P, s);
 }
 
-template <int C, int CA, int O, bool ADD>
+template <int C, int CA, int O, bool ADD, bool BF>
 static int run_epilogue(const EpiArgs& a, hipStream_t s) {
     constexpr int TH = kEpiThreads;
     constexpr size_t lds = epi_lds_bytes(C, CA, O);
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     // as many workgroups per CU as the registers the kernel is compiled for allow
     const dim3 grid(persistent_grid(tiles, lds, epi_waves(C, CA, O, ADD) / 2));
-    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, O, ADD>, grid, lds, s, &a, 0)) return st;
+    if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, O, ADD, BF>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((epilogue_kernel<C, CA, O, ADD>), grid, dim3(TH), lds, s, a);
+    hipLaunchKernelGGL((epilogue_kernel<C, CA, O, ADD, BF>), grid, dim3(TH), lds, s, a);
     stage_mark(s, 1);
     return launch_status("trimul_epilogue");
 }
 
-template <int C, int CA>
+template <int C, int CA, bool BF>
 static int epilogue_dispatch_o(const EpiArgs& a, bool add, hipStream_t s) {
-    if (a.O == 64) return add ? run_epilogue<C, CA, 64, true>(a, s) : run_epilogue<C, CA, 64, false>(a, s);
-    return add ? run_epilogue<C, CA, 128, true>(a, s) : run_epilogue<C, CA, 128, false>(a, s);
+    if (a.O == 64) return add ? run_epilogue<C, CA, 64, true, BF>(a, s) : run_epilogue<C, CA, 64, false, BF>(a, s);
+    return add ? run_epilogue<C, CA, 128, true, BF>(a, s) : run_epilogue<C, CA, 128, false, BF>(a, s);
 }
 
-template <int C>
+template <int C, bool BF>
 static int epilogue_dispatch(const EpiArgs& a, int64_t CA, bool add, hipStream_t s) {
-    return CA == 64 ? epilogue_dispatch_o<C, 64>(a, add, s) : epilogue_dispatch_o<C, 128>(a, add, s);
+    return CA == 64 ? epilogue_dispatch_o<C, 64, BF>(a, add, s) : epilogue_dispatch_o<C, 128, BF>(a, add, s);
 }
 
 extern "C" int clk_trimul_epilogue(clk_stream stream, const clk_buffer* x_cm, const clk_buffer* x,
@@ -1597,8 +1621,9 @@ extern "C" int clk_trimul_epilogue(clk_stream stream, const clk_buffer* x_cm, co
                                    const clk_buffer* bg, const clk_buffer* keep, const clk_buffer* out,
                                    float eps, int32_t add_input, int32_t has_keep) {
     const clk_buffer* bufs[] = {x_cm, x, in_scale, in_offset, ln_scale, ln_offset, woT, bo, wgT, bg, keep, out};
-    const int types[] = {CLK_F32, CLK_F16, CLK_F32, CLK_F32, CLK_F32, CLK_F32,
-                         CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    const int at = act_type(x);
+    const int types[] = {CLK_F32, at, CLK_F32, CLK_F32, CLK_F32, CLK_F32,
+                         CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, at};
     if (int st = check_types("trimul_epilogue", bufs, types, 12)) return st;
     if (x_cm->rank != 2 || x->rank != 2 || woT->rank != 2 || x->dims[0] != x_cm->dims[1] ||
         woT->dims[1] != x_cm->dims[0]) {
@@ -1621,10 +1646,15 @@ extern "C" int clk_trimul_epilogue(clk_stream stream, const clk_buffer* x_cm, co
               f16p(woT), f16p(bo), f16p(wgT), f16p(bg), has_keep ? f16p(keep) : nullptr,
               static_cast<half_t*>(out->data), (int)M, (int)O, eps};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    return C == 64 ? epilogue_dispatch<64>(a, CA, add_input, s) : epilogue_dispatch<128>(a, CA, add_input, s);
+    if (at == CLK_BF16) {
+        return C == 64 ? epilogue_dispatch<64, true>(a, CA, add_input, s)
+                       : epilogue_dispatch<128, true>(a, CA, add_input, s);
+    }
+    return C == 64 ? epilogue_dispatch<64, false>(a, CA, add_input, s)
+                   : epilogue_dispatch<128, false>(a, CA, add_input, s);
 }
 
-template <int K, bool LN>
+template <int K, bool LN, bool BF>
 static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     ProjArgs a = a0;
     // columns per workgroup: all of them while the weights fit beside the tile in LDS
@@ -1649,9 +1679,9 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
             const dim3 rgrid(persistent_grid(tiles, rlds, K == 64 ? 2 : 1));
 #define CLK_PROJ_ROWS(N_)                                                                              \
             if (a.n == N_) {                                                                           \
-                if (int st = launch_fused(what, proj_rows_kernel<K, N_>, rgrid, rlds, s, &a, 0)) return st; \
+                if (int st = launch_fused(what, proj_rows_kernel<K, N_, BF>, rgrid, rlds, s, &a, 0)) return st; \
                 stage_mark(s, 0);                                                                      \
-                hipLaunchKernelGGL((proj_rows_kernel<K, N_>), rgrid, dim3(kProjThreads), rlds, s, a);  \
+                hipLaunchKernelGGL((proj_rows_kernel<K, N_, BF>), rgrid, dim3(kProjThreads), rlds, s, a); \
                 stage_mark(s, 1);                                                                      \
                 return launch_status(what);                                                            \
             }
@@ -1663,33 +1693,33 @@ static int run_proj(const ProjArgs& a0, hipStream_t s, const char* what) {
     const bool fast = a.keep == nullptr && a.n % a.cols == 0 && pairs % TW == 0 &&
                       (pairs / TW == 1 || pairs / TW == 2);
     if (fast && pairs / TW == 1) {
-        if (int st = launch_fused(what, proj_fast_kernel<K, LN, TH, 1>, grid, lds, s, &a, 0)) return st;
+        if (int st = launch_fused(what, proj_fast_kernel<K, LN, TH, 1, BF>, grid, lds, s, &a, 0)) return st;
     } else if (fast) {
-        if (int st = launch_fused(what, proj_fast_kernel<K, LN, TH, 2>, grid, lds, s, &a, 0)) return st;
+        if (int st = launch_fused(what, proj_fast_kernel<K, LN, TH, 2, BF>, grid, lds, s, &a, 0)) return st;
     } else {
-        if (int st = launch_fused(what, proj_kernel<K, LN, TH>, grid, lds, s, &a, 0)) return st;
+        if (int st = launch_fused(what, proj_kernel<K, LN, TH, BF>, grid, lds, s, &a, 0)) return st;
     }
     stage_mark(s, 0);
     if (fast && pairs / TW == 1) {
-        hipLaunchKernelGGL((proj_fast_kernel<K, LN, TH, 1>), grid, dim3(TH), lds, s, a);
+        hipLaunchKernelGGL((proj_fast_kernel<K, LN, TH, 1, BF>), grid, dim3(TH), lds, s, a);
     } else if (fast) {
-        hipLaunchKernelGGL((proj_fast_kernel<K, LN, TH, 2>), grid, dim3(TH), lds, s, a);
+        hipLaunchKernelGGL((proj_fast_kernel<K, LN, TH, 2, BF>), grid, dim3(TH), lds, s, a);
     } else {
-        hipLaunchKernelGGL((proj_kernel<K, LN, TH>), grid, dim3(TH), lds, s, a);
+        hipLaunchKernelGGL((proj_kernel<K, LN, TH, BF>), grid, dim3(TH), lds, s, a);
     }
     stage_mark(s, 1);
     return launch_status(what);
 }
 
-template <int K, int N, bool RES>
+template <int K, int N, bool RES, bool BF>
 static int run_outproj(const ProjArgs& a, hipStream_t s) {
     constexpr size_t lds = (size_t)(N * K + kTileRows * K) * 2;
     const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
     // two workgroups per CU: the registers the kernel is compiled for allow no more
     const dim3 grid(persistent_grid(tiles, lds, 2));
-    if (int st = launch_fused("output_projection", outproj_kernel<K, N, RES>, grid, lds, s, &a, 0)) return st;
+    if (int st = launch_fused("output_projection", outproj_kernel<K, N, RES, BF>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((outproj_kernel<K, N, RES>), grid, dim3(kProjThreads), lds, s, a);
+    hipLaunchKernelGGL((outproj_kernel<K, N, RES, BF>), grid, dim3(kProjThreads), lds, s, a);
     stage_mark(s, 1);
     return launch_status("output_projection");
 }
@@ -1699,7 +1729,9 @@ extern "C" int clk_ln_projection(clk_stream stream, const clk_buffer* x, const c
                                  const clk_buffer* keep, const clk_buffer* p, const clk_buffer* bias,
                                  float eps, int64_t n, int64_t heads, int32_t has_keep) {
     const clk_buffer* bufs[] = {x, scale, offset, wT, wbT, keep, p, bias};
-    const int types[] = {CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    const int at = act_type(x);
+    const int types[] = {at, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, opt_act_type(p, n > 0, at),
+                         opt_act_type(bias, heads > 0, at)};
     if (int st = check_types("ln_projection", bufs, types, 8)) return st;
     if (x->rank != 2) return invalid("ln_projection: x must be [M,K]");
     const int64_t M = x->dims[0], K = x->dims[1];
@@ -1732,7 +1764,12 @@ extern "C" int clk_ln_projection(clk_stream stream, const clk_buffer* x, const c
     a.heads = (int)heads;
     a.eps = eps;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    return K == 64 ? run_proj<64, true>(a, s, "ln_projection") : run_proj<128, true>(a, s, "ln_projection");
+    if (at == CLK_BF16) {
+        return K == 64 ? run_proj<64, true, true>(a, s, "ln_projection")
+                       : run_proj<128, true, true>(a, s, "ln_projection");
+    }
+    return K == 64 ? run_proj<64, true, false>(a, s, "ln_projection")
+                   : run_proj<128, true, false>(a, s, "ln_projection");
 }
 
 extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, const clk_buffer* wT,
@@ -1740,7 +1777,8 @@ extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, con
                                      const clk_buffer* keep, const clk_buffer* out, int32_t has_residual,
                                      int32_t has_keep) {
     const clk_buffer* bufs[] = {o, wT, b, residual, keep, out};
-    const int types[] = {CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    const int at = act_type(o);
+    const int types[] = {at, CLK_F16, CLK_F16, opt_act_type(residual, has_residual, at), CLK_F16, at};
     if (int st = check_types("output_projection", bufs, types, 6)) return st;
     if (o->rank != 2 || wT->rank != 2 || wT->dims[1] != o->dims[1]) {
         return invalid("output_projection: o must be [M,K] and wT [N,K]");
@@ -1768,23 +1806,28 @@ extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, con
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 #define CLK_OUTPROJ(K_, N_)                                                                            \
     if (K == K_ && N == N_) {                                                                          \
-        return has_residual ? run_outproj<K_, N_, true>(a, s) : run_outproj<K_, N_, false>(a, s);      \
+        if (at == CLK_BF16) {                                                                          \
+            return has_residual ? run_outproj<K_, N_, true, true>(a, s)                                \
+                                : run_outproj<K_, N_, false, true>(a, s);                              \
+        }                                                                                              \
+        return has_residual ? run_outproj<K_, N_, true, false>(a, s)                                   \
+                            : run_outproj<K_, N_, false, false>(a, s);                                 \
     }
     CLK_OUTPROJ(64, 64) CLK_OUTPROJ(64, 128) CLK_OUTPROJ(128, 64) CLK_OUTPROJ(128, 128)
 #undef CLK_OUTPROJ
     return invalid("output_projection: K and N must be 64 or 128");
 }
 
-template <int C, bool ADD>
+template <int C, bool ADD, bool BF>
 static int run_transition(const TransArgs& a, hipStream_t s) {
     using T = TransTile<C>;
     constexpr int TH = trans_threads(C);
     const size_t lds = (size_t)(kTransRows * C + T::kW1 + T::kW2) * 2 + (size_t)(3 * C + a.H) * 4;
     const int64_t tiles = (a.M + kTransRows - 1) / kTransRows;
     const dim3 grid(persistent_grid(tiles, lds, trans_per_cu(C)));
-    if (int st = launch_fused("transition", transition_kernel<C, ADD, TH>, grid, lds, s, &a, 0)) return st;
+    if (int st = launch_fused("transition", transition_kernel<C, ADD, TH, BF>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
-    hipLaunchKernelGGL((transition_kernel<C, ADD, TH>), grid, dim3(TH), lds, s, a);
+    hipLaunchKernelGGL((transition_kernel<C, ADD, TH, BF>), grid, dim3(TH), lds, s, a);
     stage_mark(s, 1);
     return launch_status("transition");
 }
@@ -1794,7 +1837,8 @@ extern "C" int clk_transition(clk_stream stream, const clk_buffer* x, const clk_
                               const clk_buffer* w2T, const clk_buffer* b2, const clk_buffer* keep,
                               const clk_buffer* out, float eps, int32_t add_input, int32_t has_keep) {
     const clk_buffer* bufs[] = {x, scale, offset, w1T, b1, w2T, b2, keep, out};
-    const int types[] = {CLK_F16, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16};
+    const int at = act_type(x);
+    const int types[] = {at, CLK_F32, CLK_F32, CLK_F16, CLK_F16, CLK_F16, CLK_F16, CLK_F16, at};
     if (int st = check_types("transition", bufs, types, 9)) return st;
     if (x->rank != 2 || w1T->rank != 2 || w1T->dims[1] != x->dims[1]) {
         return invalid("transition: x must be [M,C] and w1T [H,C]");
@@ -1814,7 +1858,12 @@ extern "C" int clk_transition(clk_stream stream, const clk_buffer* x, const clk_
     TransArgs a{f16p(x), f32p(scale), f32p(offset), f16p(w1T), f16p(b1), f16p(w2T), f16p(b2),
                 has_keep ? f16p(keep) : nullptr, static_cast<half_t*>(out->data), (int)M, (int)H, eps};
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (C == 64) return add_input ? run_transition<64, true>(a, s) : run_transition<64, false>(a, s);
-    if (C == 128) return add_input ? run_transition<128, true>(a, s) : run_transition<128, false>(a, s);
-    return add_input ? run_transition<256, true>(a, s) : run_transition<256, false>(a, s);
+    if (at == CLK_BF16) {
+        if (C == 64) return add_input ? run_transition<64, true, true>(a, s) : run_transition<64, false, true>(a, s);
+        if (C == 128) return add_input ? run_transition<128, true, true>(a, s) : run_transition<128, false, true>(a, s);
+        return add_input ? run_transition<256, true, true>(a, s) : run_transition<256, false, true>(a, s);
+    }
+    if (C == 64) return add_input ? run_transition<64, true, false>(a, s) : run_transition<64, false, false>(a, s);
+    if (C == 128) return add_input ? run_transition<128, true, false>(a, s) : run_transition<128, false, false>(a, s);
+    return add_input ? run_transition<256, true, false>(a, s) : run_transition<256, false, false>(a, s);
 }

@@ -26,7 +26,7 @@ extern "C" {
 
 typedef struct ihipStream_t* clk_stream; /* a hipStream_t; NULL is the null stream */
 
-enum clk_dtype { CLK_S32 = 4, CLK_U8 = 6, CLK_F16 = 10, CLK_F32 = 11 };
+enum clk_dtype { CLK_S32 = 4, CLK_U8 = 6, CLK_F16 = 10, CLK_F32 = 11, CLK_BF16 = 16 };
 
 enum clk_status { CLK_OK = 0, CLK_INVALID_ARGUMENT = 3, CLK_INTERNAL = 13 };
 
@@ -118,6 +118,14 @@ int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int64_t Sq, int
                            int64_t D, int64_t* plan, int32_t count);
 
 /* ---- LayerNorm-fused pair-stack projections (reference cuda/volta_fused_ffi.h) --------- */
+
+/* Activation types, an addition to the reference (whose handlers bind F16 only): the activation
+ * buffers of each entry point below (x, o, residual and every activation result: left, right,
+ * out, p, bias) may be BF16 instead of F16, all together; weights, biases and keep stay F16 and
+ * LayerNorm parameters F32. A BF16 input is read exactly into fp32, the LayerNorm output (and
+ * o, and the transition's hidden activation) enter the matrix cores as fp16, and the results
+ * are rounded to BF16 once. A mix of F16 and BF16 activations is CLK_INVALID_ARGUMENT. The XLA
+ * FFI handlers keep the reference's F16-only binding. */
 
 /* VoltaLnGdp (volta_fused_ffi.h:42-80, handler 337-351): left, right [P/2, M] = the two halves
  * of max(mask,0) * (y@wp + bp) * sigmoid(y@wg + bg), channel major, y = LN(x).

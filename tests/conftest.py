@@ -66,6 +66,13 @@ def ulp16(x):
     return 2.0 ** (e - 10)
 
 
+def ulp_bf16(x):
+    """One bf16 ulp at |x| (8-bit significand)."""
+    a = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
 def rel(a, b):
     """The reference tests' error metric (tests/test_attn_bwd.py:104-111)."""
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
@@ -74,14 +81,17 @@ def rel(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-3)) if a.size else 0.0
 
 
-def abs_excess(got, want, fp16_out=True):
-    """max |got - want| beyond half an fp16 ulp of want (the unavoidable output rounding)."""
+def abs_excess(got, want, fp16_out=True, bf16_out=False):
+    """max |got - want| beyond half an output ulp of want (the unavoidable output rounding):
+    an fp16 ulp, or a bf16 ulp with bf16_out."""
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     if got.size == 0:
         return 0.0
     if not np.isfinite(got).all():
         return float("inf")
     err = np.abs(got - want)
-    if fp16_out:
+    if bf16_out:
+        err = err - 0.5 * ulp_bf16(want)
+    elif fp16_out:
         err = err - 0.5 * ulp16(want)
     return float(max(err.max(), 0.0))

@@ -130,3 +130,33 @@ def test_backward_workspace_size(lib, n, h, sq, sk, d):
     sqa, ska = -(-sq // 32) * 32, -(-sk // 64) * 64
     assert size >= 4 * 2 * n * h * sqa + 2 * h * ska * sqa
     assert size % 256 == 0
+
+
+def test_fused_activation_dtypes(lib):
+    """The fused entry points take BF16 activations as a whole: x and every activation result
+    BF16 together, weights and biases still F16; a mix is rejected before any launch."""
+    BF16 = 16
+    m = 100
+    # transition: x BF16, out F16 -> rejected
+    args = [buf(BF16, m, 128), buf(F32, 128), buf(F32, 128), buf(F16, 512, 128), buf(F16, 512),
+            buf(F16, 512 * 128), buf(F16, 128), buf(F16, 1), buf(F16, m, 128)]
+    st = lib.clk_transition(None, *[a[0] for a in args], ctypes.c_float(1e-5), 0, 0)
+    assert st == 3 and "must be BF16" in lib.clk_last_error().decode()
+    # transition: a BF16 weight is rejected as well
+    args = [buf(BF16, m, 128), buf(F32, 128), buf(F32, 128), buf(BF16, 512, 128), buf(F16, 512),
+            buf(F16, 512 * 128), buf(F16, 128), buf(F16, 1), buf(BF16, m, 128)]
+    st = lib.clk_transition(None, *[a[0] for a in args], ctypes.c_float(1e-5), 0, 0)
+    assert st == 3 and "must be F16" in lib.clk_last_error().decode()
+    # output projection: BF16 o and out with an F16 residual -> rejected
+    args = [buf(BF16, m, 64), buf(F16, 64, 64), buf(F16, 64), buf(F16, m, 64), buf(F16, 1),
+            buf(BF16, m, 64)]
+    st = lib.clk_output_projection(None, *[a[0] for a in args], 1, 0)
+    assert st == 3 and "must be BF16" in lib.clk_last_error().decode()
+    # all-BF16 activations with M == 0 pass validation and launch nothing
+    args = [buf(BF16, 0, 64), buf(F16, 64, 64), buf(F16, 64), buf(BF16, 1), buf(F16, 1), buf(BF16, 0, 64)]
+    assert lib.clk_output_projection(None, *[a[0] for a in args], 0, 0) == 0
+    # ln_gdp: BF16 x with F16 left/right -> rejected
+    args = [buf(BF16, m, 64), buf(F32, 64), buf(F32, 64), buf(F16, 128, 64), buf(F16, 128),
+            buf(F16, 128, 64), buf(F16, 128), buf(F16, m), buf(F16, 64, m), buf(F16, 64, m)]
+    st = lib.clk_ln_gdp(None, *[a[0] for a in args], ctypes.c_float(1e-5))
+    assert st == 3 and "must be BF16" in lib.clk_last_error().decode()

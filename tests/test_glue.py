@@ -81,7 +81,8 @@ def test_fused_available_declines():
     assert not torch_ops.fused_available("ln_projection", f16, 128, 32)
     assert not torch_ops.fused_available("output_projection", f16, 256, 256)
     assert not torch_ops.fused_available("ln_projection", f16, 256, 256)
-    assert not torch_ops.fused_available("ln_projection", torch.bfloat16, 128, 128)
+    assert torch_ops.fused_available("ln_projection", torch.bfloat16, 128, 128)  # an addition here
+    assert not torch_ops.fused_available("ln_projection", torch.float32, 128, 128)
     assert not torch_ops.fused_available("transition", f16, 512, 2048)
     assert not torch_ops.fused_available("transition", f16, 128, 384)
     assert torch_ops.fused_available("transition", f16, 256, 1024)

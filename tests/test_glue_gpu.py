@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from colabfold_legacy_kernels import layouts, torch_ops
-from conftest import record_error
+from conftest import abs_excess, record_error
 from oracle import attention as ora
 from oracle import fused as orf
 from test_attention_gpu import GRAD_ATOL, OUT_ATOL, REL_TOL, check, dev, host, inputs
@@ -160,3 +160,36 @@ def test_fused_natural_layouts(hip):
     want = orf.trimul_epilogue(x_cm, x, sc, of, lsc, lof, weo.T, beo, wge.T, bge, None, 1e-5, True)
     raw, e, r = record_error("glue epilogue", "out", host(out)[0], want)
     assert e <= OUT_ATOL
+
+
+def test_fused_bf16_model(hip):
+    """A bf16 model: bf16 activations and bf16 weights. The glue casts weights and biases to fp16
+    (exact for weights of fp16 range) and keeps the activations bf16; the results are bf16 and
+    agree bit for bit with the C ABI called on the fp16-cast, re-laid-out weights."""
+    rng = np.random.default_rng(27)
+    m, c = 4101, 128
+    bf = lambda *shape, s=1.0: torch.from_numpy(rng.standard_normal(shape) * s).to(torch.bfloat16).cuda()
+    x = bf(1, m, c, s=2.0)
+    sc, of = (t.cuda() for t in (torch.from_numpy(f32(rng, c, mean=1.0)), torch.from_numpy(f32(rng, c))))
+    w1, b1, w2, b2 = bf(c, 4 * c, s=c ** -.5), bf(4 * c, s=.1), bf(4 * c, c, s=(4 * c) ** -.5), bf(c, s=.1)
+    assert torch_ops.fused_available("transition", x.dtype, c, 4 * c)
+    out = torch_ops.transition(x, sc, of, w1, b1, w2, b2)
+    assert out.dtype == torch.bfloat16 and out.shape == (1, m, c)
+    h = lambda t: t.to(torch.float16)
+    out2 = hip.transition(x.reshape(m, c), sc, of, layouts.linear_T(h(w1)), h(b1),
+                          layouts.w2_blocked(h(w2)), h(b2))
+    assert torch.equal(out.reshape(m, c), out2)
+    w1n, w2n = h(w1).cpu().numpy(), h(w2).cpu().numpy()
+    want = orf.transition(x[0].double().cpu().numpy(), sc.cpu().numpy(), of.cpu().numpy(), w1n.T,
+                          h(b1).cpu().numpy(), orf.w2_blocked(w2n), h(b2).cpu().numpy(), None, 1e-5,
+                          False)
+    got = out[0].double().cpu().numpy()
+    assert abs_excess(got, want, bf16_out=True) <= 2e-3
+    # output_projection written over a bf16 residual
+    o, wo, bo, res = bf(m, c), bf(c, c, s=.1), bf(c, s=.1), bf(m, c)
+    res0 = res.clone()
+    out = torch_ops.output_projection(o, wo, bo, residual=res)
+    assert out.data_ptr() == res.data_ptr() and out.dtype == torch.bfloat16
+    want = orf.output_projection(o.double().cpu().numpy(), h(wo).cpu().numpy().T,
+                                 h(bo).cpu().numpy(), res0.double().cpu().numpy(), None)
+    assert abs_excess(out.double().cpu().numpy(), want, bf16_out=True) <= 2e-3
