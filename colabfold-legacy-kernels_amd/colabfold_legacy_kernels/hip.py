@@ -169,9 +169,9 @@ def attention_bwd_workspace(q, k):
 
 def attention_bwd_plan(n, h, sq, sk, d, device=0):
     """The backward's launch plan on `device` (a diagnostic for tests and the bench)."""
-    vals = (ctypes.c_int64 * 5)()
-    _check(lib().clk_attention_bwd_plan(device, n, h, sq, sk, d, vals, 5))
-    return dict(zip(("row_groups", "chunk", "chunks", "passes", "windows"), list(vals)))
+    vals = (ctypes.c_int64 * 6)()
+    _check(lib().clk_attention_bwd_plan(device, n, h, sq, sk, d, vals, 6))
+    return dict(zip(("row_groups", "chunk", "chunks", "passes", "windows", "registers"), list(vals)))
 
 
 def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale, want_dbias=True, workspace=None,

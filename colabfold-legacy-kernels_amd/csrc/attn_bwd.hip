@@ -10,8 +10,9 @@
 //
 // Where the reference adds dQ and dBias with fp32 atomics into global memory, this backward is
 // three kernels with no atomics, so every result is bit-identical from run to run:
-//   biast_kernel  bias transposed to [H][keys][queries] (fp16, zero-padded), so a dK/dV lane
-//                 reads its eight queries' bias at its key with one 16-byte load.
+//   biast_kernel  log2e bias transposed to [H][keys][queries] (fp32, zero-padded), so a dK/dV
+//                 lane reads its eight queries' bias at its key with two 16-byte loads and
+//                 s2 = scale log2e S + log2e bias is one fma.
 //   dq_kernel     one workgroup per (n, h, 128 queries), looping over key tiles as the forward
 //                 does: dQ^T = K^T dS^T accumulates in registers; it also writes delta and lse2
 //                 padded to whole 32-query tiles (0 and +inf past Sq).
@@ -43,13 +44,16 @@ struct BwdArgs {
     // workspace [N, H, SqA / 32][64]: per 32-query tile, -lse2 / c1 of its queries (-inf past
     // Sq), then -rowsum(out * dout) of them (0 past Sq)
     float* qstat;
-    half_t* biast;   // workspace [H, SkA, SqA]: bias[h][q][key], 0 outside
+    // workspace [H, SkA + 1, SqB]: log2e bias[h][q][key] (fp32), -inf outside; row SkA of each
+    // head holds the masked logit (log2e kMaskedLogit), the bias a dead key's lane reads
+    float* biast;
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
     // workspace [2][windows][N][H][Sk][D]: with more than one query window, each window's fp32
     // dK (unscaled) and dV sums over its queries, added up in window order by dkdv_sum_kernel
     float* dkv;
     int N, H, Sq, Sk, D;
     int SqA, SkA;    // Sq rounded up to 32, Sk rounded up to 64
+    int SqB;         // queries per transposed-bias row: SqA, or 32 QT for the register kernel
     int kblocks;     // ceil(Sk / 64)
     int chunk;       // batch rows per dkdv workgroup
     int chunks;
@@ -454,7 +458,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 
     const float scale = a.scale;
-    const float c1s = a.c1s;  // scale, or the stand-in for a negligible scale (K is zero then)
+    const float c1 = a.c1;  // scale log2e, or the stand-in for a negligible scale (K is zero then)
 
     // Step `it` of a row pass is query tile tile_of(it) of the group's row for that pass; a step
     // past the row's tiles, or a pass past n_end, is idle. Every load below is issued
@@ -484,10 +488,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     // one of the tile's query terms, [-lse2 / c1 of its 32 queries][-delta of them]: lane i of
     // 16-lane row g holds -lse2 / c1 of query 8 g + i for i < 8, -delta of query 8 g + i - 8 above
     const uint32_t st_off = 4u * (uint32_t)(r16 < 8 ? 8 * g + r16 : T::kBQ + 8 * g + r16 - 8);
-    // this lane's eight queries' bias at its key
+    // this lane's eight queries' log2e bias at its key
     const char* const bt_base =
-        reinterpret_cast<const char*>(a.biast + ((int64_t)h * a.SkA + kblk * T::kBK) * a.SqA);
-    const uint32_t bt_off = (uint32_t)(klocal * a.SqA + 8 * g) * 2u;
+        reinterpret_cast<const char*>(a.biast + ((int64_t)h * (a.SkA + 1) + kblk * T::kBK) * a.SqB);
+    const uint32_t bt_off = (uint32_t)(klocal * a.SqB + 8 * g) * 4u;
 
     // A step's Q / dO chunks: two register sets, one per step parity, fetched two steps ahead of
     // their stage. The bias and the query term: two register sets likewise, two steps ahead of
@@ -496,7 +500,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         half8 s[T::kCPT];
     };
     Chunks ch0, ch1;
-    half8 bt0, bt1;
+    float8v bt0, bt1;
     float sq0, sq1;
     // The chunk and bias prefetches walk the steps with cursors of their own, ahead of the
     // step being computed; a cursor past the last pass reads zeros (chunks) or a valid tile
@@ -535,9 +539,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const int64_t nh = (int64_t)(n < n_end ? n : n_begin) * a.H + h;
         bc_st = reinterpret_cast<const char*>(a.qstat + nh * a.SqA * 2);
     };
-    const auto fetch_c = [&](half8& d, float& sq) {
+    const auto fetch_c = [&](float8v& d, float& sq) {
         const int q0 = (wt0 + tile_of(bc_it)) * T::kBQ;
-        d = *reinterpret_cast<const half8*>(bt_base + q0 * 2 + bt_off);
+        d = *reinterpret_cast<const float8v*>(bt_base + q0 * 4 + bt_off);
         sq = *reinterpret_cast<const float*>(bc_st + q0 * 8 + st_off);
         if (++bc_it == qsteps) {
             bc_it = 0;
@@ -594,7 +598,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     // with the step two on once consumed; after its S and dP products it stages the next step
     // from the chunk set of that parity and refills the set with the step three on (steps past
     // the end load the last step again, unused)
-    const auto step = [&](int it, Chunks& next, half8& bt, float& sq) {
+    const auto step = [&](int it, Chunks& next, float8v& bt, float& sq) {
         const int buf = it & 1, q0 = tile_of(it) * T::kBQ;  // within the window
         const bool valid = nv && it < qtiles;
         const half_t* Qs = stage0 + buf * kBufStride;
@@ -636,13 +640,13 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
                 s = mfma16x16x32(qa, kop[ks], s);
                 dp[qb] = mfma16x16x32(oa, vop[ks], dp[qb]);
             }
-            // s2 = log2e (scale S + bias); a dead key (K zero) takes the masked logit
+            // s2 = scale log2e S + log2e bias; a dead key (K zero) takes the masked logit
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1s, (float)bt[4 * qb + i]) * kLog2e;
+            for (int i = 0; i < 4; ++i) x[4 * qb + i] = fmaf(s[i], c1, bt[4 * qb + i]);
             if (!all_alive) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    x[4 * qb + i] = alive ? x[4 * qb + i] : fmaf(s[i], c1s, kMaskedLogit) * kLog2e;
+                    x[4 * qb + i] = alive ? x[4 * qb + i] : fmaf(s[i], c1, kMaskedLogit2);
                 }
             }
         }
@@ -760,6 +764,283 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// dK, dV and the dBias partials where D == 32 and Sq <= 32 QT (QT in {4, 8, 12}): the same
+// products and lane layout as attn_bwd_dkdv_kernel, arranged so that the dBias partial never
+// leaves registers. A workgroup of eight waves owns 64 keys of one head and a chunk of batch
+// rows: wave w takes key group w % 4 (16 keys) and query half w / 4 (QT / 2 tiles of 32), so the
+// dBias partial of its keys over its queries is QT / 2 x 8 registers per lane for the whole
+// chunk. The two halves' dK and dV sums of a row meet in LDS once per row (one fixed order). The
+// workgroup's transposed log2e bias (64 keys plus the masked-logit row, the same for every row)
+// is read into LDS once, so the per-tile bias reads are LDS reads.
+//
+// The query loop is unrolled (every register index is static) and branch-free. The transposed
+// bias is -inf for every query past Sq up to 32 QT, so a padded or absent query has p = 0 and
+// dS = 0 whatever its (zero) Q, dO and query terms. A dead key (masked, or past Sk) needs no
+// selects either: its lane reads the masked-logit bias row instead of its own (so with K zero its
+// s2 is the masked logit's), and reads its -delta from a zeroed LDS area (so with V zero its dP,
+// and with it dS, is exactly 0 while p still carries dV).
+//
+// Per step (two tiles per query half), in order: stage the next step (loaded a step ago) into the
+// other LDS buffer, issue the loads of the step after it, compute the step, barrier. The query
+// terms -lse2 / c1 and -delta of the step's tiles are staged beside them and read back as
+// float4 broadcasts (the MFMA accumulator inputs of S and dP).
+// ------------------------------------------------------------------------------------------
+// The register kernel's Q and dO tiles (32 rows of 32 halfs), in 4-byte words: LDS row R takes 16
+// words, its 16-byte chunk k at chunk k ^ ((R / 4) % 4), in order within the chunk. A row-form
+// operand (16 rows of one chunk per 16 lanes) is then one conflict-free 16-byte read.
+__device__ __forceinline__ int reg_word(int R, int col) {
+    return 16 * R + 4 * ((col >> 3) ^ ((R >> 2) & 3)) + 2 * ((col >> 2) & 1);
+}
+
+// dkdv_operand_tr for the register kernel's layout (D = 32, d block db of 2)
+__device__ __forceinline__ half8 reg_operand_tr(const half_t* tile, int g, int lane16, int db) {
+    const int j = lane16 >> 2, c = lane16 & 3;
+    const int col = 4 * db + 8 * c;
+    const half4 lo = lds_read_tr16(tile + 2 * reg_word(perm_row(8 * g + j, 8), col));
+    const half4 hi = lds_read_tr16(tile + 2 * reg_word(perm_row(8 * g + 4 + j, 8), col));
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+template <int QT>
+struct RegTile {
+    static constexpr int DP = 32;
+    static constexpr int HT = QT / 2;                // tiles per query half
+    static constexpr int kSteps = HT / 2;            // steps per row, two tiles per half each
+    static constexpr int kTile = 32 * DP;            // halfs of a 32-query Q (or dO) tile
+    static constexpr int kOs = kTile + 64;           // the dO tile, after a 128-byte gap
+    static constexpr int kSub = kOs + kTile;         // halfs of one tile's Q and dO
+    static constexpr int kBuf = 4 * kSub;            // halfs of a step: [half][tile]
+    static constexpr int SqB = 32 * QT;              // transposed-bias row length
+    static constexpr int kBRow = SqB + 4;            // its LDS row stride (floats)
+    static constexpr int kSlots = kSteps == 1 ? 2 : 1;  // dK/dV meeting slots, by row parity
+    static constexpr int kLdsBytes = 65 * kBRow * 4 + 2 * kBuf * 2 + 1024 * 4 + kSlots * 4 * 4 * 64 * 16;
+};
+
+template <int QT, bool DBIAS>
+__global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
+    using T = RegTile<QT>;
+    static_assert(QT % 4 == 0 && QT <= 12, "whole steps of two tiles per half");
+    constexpr int DP = T::DP, HT = T::HT, kSteps = T::kSteps, kSub = T::kSub, kOs = T::kOs;
+    constexpr int kBuf = T::kBuf, SqB = T::SqB, kBRow = T::kBRow;
+    __shared__ __attribute__((aligned(16))) float bias_l[65 * kBRow];  // rows: 64 keys, masked
+    __shared__ __attribute__((aligned(16))) half_t lds[2 * kBuf];
+    // query terms [buf][half][tile][-lse2 / c1 x 32, -delta x 32], then 512 zeros
+    __shared__ __attribute__((aligned(16))) float qterms[1024];
+    // the query half 1 waves' dK / dV sums of a row: [slot][key group][float4 j][lane]
+    __shared__ __attribute__((aligned(16))) float4 red[T::kSlots * 4 * 4 * 64];
+
+    const int item = xcd_item(blockIdx.x, gridDim.x);
+    // head-major order: an XCD's run of items reads few heads' bias columns
+    const int kblk = item % a.kblocks, rest = item / a.kblocks;
+    const int c = rest % a.chunks, h = rest / a.chunks;
+    const int n_begin = c * a.chunk;
+    const int rows = min(a.N, n_begin + a.chunk) - n_begin;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int kg = wave & 3, qh = wave >> 2;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int klocal = kg * 16 + r16;
+    const int key = kblk * 64 + klocal;
+    const bool kin = key < a.Sk;
+    const float c1 = a.c1;
+
+    // the workgroup's transposed bias: rows kblk 64 .. + 63 and the masked-logit row SkA
+    {
+        const float* src = a.biast + (int64_t)h * (a.SkA + 1) * SqB;
+        for (int idx = tid; idx < 65 * (SqB / 4); idx += 512) {
+            const int r = idx / (SqB / 4), c4 = idx - r * (SqB / 4);
+            const int srow = r < 64 ? kblk * 64 + r : a.SkA;
+            *reinterpret_cast<float4*>(bias_l + r * kBRow + 4 * c4) =
+                *reinterpret_cast<const float4*>(src + (int64_t)srow * SqB + 4 * c4);
+        }
+    }
+    if (tid < 128) reinterpret_cast<float4*>(qterms + 512)[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // this wave's staging share of a step: tile (half sqh, tile si) of tensor (Q, dO), scalars,
+    // rows crow and crow + 16 at a fixed column
+    const int ti = wave >> 1, tensor = wave & 1, sqh = ti >> 1, si = ti & 1;
+    const int crow = lane >> 2, ccol = (lane & 3) * 8;
+    const uint32_t cvoff = (uint32_t)((crow * DP + ccol) * 2);
+    const int cdst0 = (2 * sqh + si) * kSub + tensor * kOs + 2 * reg_word(perm_row(crow, 8), ccol);
+    const int cdst1 = (2 * sqh + si) * kSub + tensor * kOs + 2 * reg_word(perm_row(crow + 16, 8), ccol);
+    const half_t* const csrc = tensor ? a.dout : a.q;
+    // wave 0 also stages the step's query terms: lane l, tile l / 16 of [half][tile], 4 floats
+    const int qt_t = lane >> 4;
+    const uint32_t qt_f = (uint32_t)(4 * (lane & 15));
+
+    // row `pass` of the chunk, clamped to a real row past the end (its data is staged, never read)
+    const auto row_nh = [&](int pass) -> int64_t {
+        return (int64_t)(n_begin + (pass < rows ? pass : 0)) * a.H + h;
+    };
+    half8 chk[2];
+    float4 qst;
+    const auto fetch_s = [&](int pass, int step) {
+        const int64_t nh = row_nh(pass);
+        const int q0 = 32 * (sqh * HT + 2 * step + si);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<half_t*>(csrc + (nh * a.Sq + q0) * DP), 0, max(a.Sq - q0, 0) * DP * 2, 0x00020000);
+        chk[0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff, 0, 0));
+        chk[1] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff + 16u * DP * 2u, 0, 0));
+        if (wave == 0) {
+            const int tg = (qt_t >> 1) * HT + 2 * step + (qt_t & 1);
+            const auto rq = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(a.qstat + nh * a.SqA * 2), 0, a.SqA * 2 * 4, 0x00020000);
+            qst = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                rq, ((uint32_t)(64 * tg) + qt_f) * 4u, 0, 0));
+        }
+    };
+    const auto stage = [&](int buf) {
+        half_t* dst = lds + buf * kBuf;
+        *reinterpret_cast<half8*>(dst + cdst0) = chk[0];
+        *reinterpret_cast<half8*>(dst + cdst1) = chk[1];
+        if (wave == 0) *reinterpret_cast<float4*>(qterms + buf * 256 + 4 * lane) = qst;
+    };
+
+    // K and V of the next row as B operands (lane column = key, slots d = 8 g + j), its mask byte
+    half8 kopn, vopn;
+    uint32_t mbn = 0u;
+    const auto fetch_kv = [&](int pass) {
+        const int64_t nh = row_nh(pass);
+        const int kc = kin ? key : 0;
+        mbn = (uint32_t)a.kmask[(nh / a.H) * a.Sk + kc];
+        const int64_t off = (nh * a.Sk + kc) * DP + 8 * g;
+        kopn = bld8(a.k + off);
+        vopn = bld8(a.v + off);
+    };
+
+    float dbias[HT][8];
+    if constexpr (DBIAS) {
+#pragma unroll
+        for (int u = 0; u < HT; ++u)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dbias[u][j] = 0.f;
+    }
+
+    if (rows > 0) {
+        fetch_kv(0);
+        fetch_s(0, 0);
+        stage(0);
+        fetch_s(1 / kSteps, 1 % kSteps);
+    }
+    __syncthreads();
+
+    for (int pass = 0; pass < rows; ++pass) {
+        const int n = n_begin + pass;
+        const bool alive = kin && mbn != 0u;
+        const half8 kop = alive && a.kscale ? kopn : bzero8();
+        const half8 vop = alive ? vopn : bzero8();
+        // a dead key's lane: the masked-logit bias row, and -delta from the zeroed area
+        const float* const brow = bias_l + (alive ? klocal : 64) * kBRow + qh * HT * 32 + 8 * g;
+        const float* const qtS = qterms + qh * 128 + 8 * g;
+        const float* const qtD = qtS + 32 + (alive ? 0 : 512);
+        float4v accv[2], acck[2];
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
+            acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
+        }
+        fetch_kv(pass + 1);
+
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            const int par = (pass * kSteps + st) & 1;
+            // stage the next step (loaded a step ago), fetch the one after it
+            stage(par ^ 1);
+            fetch_s(pass + (st + 2) / kSteps, (st + 2) % kSteps);
+            const half_t* buf = lds + par * kBuf + qh * 2 * kSub;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int u = 2 * st + i;  // tile within the half
+                const half_t* Qs = buf + i * kSub;
+                const half_t* Os = Qs + kOs;
+                const int qo = par * 256 + 64 * i;
+                // S from -lse2 / c1 and dP from -delta: the lane holds queries 8 g + 4 qb + i4
+                float x[8];
+                float4v dp[2];
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    float4v sacc = *reinterpret_cast<const float4v*>(qtS + qo + 4 * qb);
+                    dp[qb] = *reinterpret_cast<const float4v*>(qtD + qo + 4 * qb);
+                    const int w = 2 * reg_word(16 * qb + r16, 8 * g);
+                    const half8 qa = *reinterpret_cast<const half8*>(Qs + w);
+                    const half8 oa = *reinterpret_cast<const half8*>(Os + w);
+                    sacc = mfma16x16x32(qa, kop, sacc);
+                    dp[qb] = mfma16x16x32(oa, vop, dp[qb]);
+                    const float4 bb = *reinterpret_cast<const float4*>(brow + 32 * u + 4 * qb);
+                    x[4 * qb + 0] = fmaf(sacc[0], c1, bb.x);
+                    x[4 * qb + 1] = fmaf(sacc[1], c1, bb.y);
+                    x[4 * qb + 2] = fmaf(sacc[2], c1, bb.z);
+                    x[4 * qb + 3] = fmaf(sacc[3], c1, bb.w);
+                }
+                half8 pb, dsb;
+                float dsf[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = exp2_fast(x[j]);
+                    dsf[j] = pin_f32(p * dp[j >> 2][j & 3]);
+                    pb[j] = (half_t)p;
+                    dsb[j] = (half_t)dsf[j];
+                }
+                if constexpr (DBIAS) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) dbias[u][j] += dsf[j];
+                }
+                // dV^T += dO^T P, dK^T += Q^T dS (k-slots queries 8 g + j, read transposed)
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    const half8 ot = reg_operand_tr(Os, g, r16, db);
+                    const half8 qt = reg_operand_tr(Qs, g, r16, db);
+                    accv[db] = mfma16x16x32(ot, pb, accv[db]);
+                    acck[db] = mfma16x16x32(qt, dsb, acck[db]);
+                }
+            }
+            if (st == kSteps - 1 && qh == 1) {
+                // this half's sums of the row, for the half 0 wave of the same keys
+                float4* r = red + ((T::kSlots == 2 ? (pass & 1) : 0) * 4 + kg) * 4 * 64 + lane;
+                r[0] = make_float4(acck[0][0], acck[0][1], acck[0][2], acck[0][3]);
+                r[64] = make_float4(acck[1][0], acck[1][1], acck[1][2], acck[1][3]);
+                r[128] = make_float4(accv[0][0], accv[0][1], accv[0][2], accv[0][3]);
+                r[192] = make_float4(accv[1][0], accv[1][1], accv[1][2], accv[1][3]);
+            }
+            __syncthreads();
+        }
+
+        if (qh == 0 && kin) {
+            // half 0 + half 1, then lane holds d = 8 g .. + 8 of its key (a masked key's dS,
+            // and so dK, is 0)
+            const float4* r = red + ((T::kSlots == 2 ? (pass & 1) : 0) * 4 + kg) * 4 * 64 + lane;
+            const float4 k0 = r[0], k1 = r[64], v0 = r[128], v1 = r[192];
+            const float ks[8] = {acck[0][0] + k0.x, acck[0][1] + k0.y, acck[0][2] + k0.z, acck[0][3] + k0.w,
+                                 acck[1][0] + k1.x, acck[1][1] + k1.y, acck[1][2] + k1.z, acck[1][3] + k1.w};
+            const float vs[8] = {accv[0][0] + v0.x, accv[0][1] + v0.y, accv[0][2] + v0.z, accv[0][3] + v0.w,
+                                 accv[1][0] + v1.x, accv[1][1] + v1.y, accv[1][2] + v1.z, accv[1][3] + v1.w};
+            const int64_t off = (((int64_t)n * a.H + h) * a.Sk + key) * DP + 8 * g;
+            half8 ok, ov;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ok[j] = (half_t)(ks[j] * a.scale);
+                ov[j] = (half_t)vs[j];
+            }
+            *reinterpret_cast<half8*>(a.dk + off) = ok;
+            *reinterpret_cast<half8*>(a.dv + off) = ov;
+        }
+    }
+
+    if constexpr (DBIAS) {
+        // the chunk's [SqA][64] partial: query 32 (qh HT + u) + 8 g + j, this lane's key column
+        const int qtiles = a.SqA / 32;
+        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * 64 + klocal;
+#pragma unroll
+        for (int u = 0; u < HT; ++u) {
+            const int ut = qh * HT + u;
+            if (ut >= qtiles) continue;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dst[(int64_t)(32 * ut + 8 * g + j) * 64] = dbias[u][j];
+        }
+    }
+}
+
 // With more than one query window: dk = fp16(scale * sum of the windows' dK sums), dv = fp16(sum
 // of their dV sums), each summed in window order, four elements per thread (D % 4 == 0).
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_sum_kernel(BwdArgs a) {
@@ -782,12 +1063,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_sum_kernel(BwdArgs a) {
     }
 }
 
-// biast[h][key][q] = bias[h][q][key] for q < Sq, key < Sk, else 0, over [H][SkA][SqA]: a
-// workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads where the bias rows
-// allow them and 16-byte stores (SqA is a multiple of 32).
+// biast[h][key][q] = log2e bias[h][q][key] in fp32 for q < Sq, key < Sk, else -inf, over
+// [H][SkA + 1][SqB]: a workgroup transposes 32 queries x 64 keys through LDS, with 16-byte loads
+// where the bias rows allow them and 16-byte stores (SqB is a multiple of 32). The workgroups of
+// key block 0 also write their queries of row SkA: log2e kMaskedLogit (q < Sq), else -inf.
 __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
     __shared__ half_t tile[32][66];
-    const int qtiles = a.SqA / 32;
+    const int qtiles = a.SqB / 32;
     const int item = blockIdx.x;
     const int qt = item % qtiles, rest = item / qtiles;
     const int kblk = rest % a.kblocks, h = rest / a.kblocks;
@@ -811,10 +1093,17 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
     __syncthreads();
     {
         const int kk = tid / 4, qc = (tid % 4) * 8;
-        half8 o;
+        float8v o;
+        const bool kok = k0 + kk < a.Sk;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = tile[qc + j][kk];
-        *reinterpret_cast<half8*>(a.biast + ((int64_t)h * a.SkA + k0 + kk) * a.SqA + q0 + qc) = o;
+        for (int j = 0; j < 8; ++j) {
+            o[j] = kok && q0 + qc + j < a.Sq ? (float)tile[qc + j][kk] * kLog2e : -INFINITY;
+        }
+        *reinterpret_cast<float8v*>(a.biast + ((int64_t)h * (a.SkA + 1) + k0 + kk) * a.SqB + q0 + qc) = o;
+        if (kblk == 0 && tid < 32) {
+            a.biast[((int64_t)h * (a.SkA + 1) + a.SkA) * a.SqB + q0 + tid] =
+                q0 + tid < a.Sq ? kMaskedLogit2 : -INFINITY;
+        }
     }
 }
 
@@ -889,11 +1178,12 @@ static int cu_count(int device) {
 
 struct BwdPlan {
     int DP = 32;
+    int QT = 0;  // query tiles of the register-partial dK/dV kernel (4, 8 or 12), 0: not used
     int QG = 1;  // query groups of the dK/dV kernel
     int kblocks = 0, chunk = 0, chunks = 0;
     int wtiles = 1, windows = 1;  // query windows of the dK/dV kernel
     size_t stage_lds = 0, dbias_lds = 0;
-    int SqA = 0, SkA = 0;
+    int SqA = 0, SkA = 0, SqB = 0;
     size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0, dkv_bytes = 0;
     std::string error;
 };
@@ -924,9 +1214,40 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     int limit = shared_limit(device);
     if (limit <= 0) limit = 64 * 1024;
     const size_t tile_bytes = (size_t)64 * 32 * sizeof(float);
+    const int64_t qtiles = std::max<int64_t>((Sq + 31) / 32, 1);
+    const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
+    if (D == 32 && qtiles <= 12) {
+        // the register-partial kernel: one workgroup of eight waves per CU, one row per pass;
+        // chunks trade rounds of workgroups against dbias partials to write and sum (one
+        // partial weighs about H kblocks / 128 row passes)
+        p.QT = qtiles <= 4 ? 4 : qtiles <= 8 ? 8 : 12;
+        p.QG = 1;
+        p.wtiles = (int)qtiles;
+        p.windows = 1;
+        const int64_t slots = (int64_t)cu_count(device);
+        const int64_t cols = std::max<int64_t>(H * p.kblocks, 1);
+        int64_t best = 1;
+        double best_cost = 1e300;
+        for (int64_t ch = 1; ch <= Nr; ++ch) {
+            const int64_t rows = (Nr + ch - 1) / ch;
+            const int64_t real = (Nr + rows - 1) / rows;
+            const int64_t rounds = (real * cols + slots - 1) / slots;
+            const double cost = (double)rounds * rows + (double)real * cols / 128.0;
+            if (cost < best_cost) {
+                best_cost = cost;
+                best = real;
+            }
+        }
+        p.chunk = (int)((Nr + best - 1) / best);
+        p.chunks = (int)((N + p.chunk - 1) / p.chunk);
+        p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));
+        p.SqB = 32 * p.QT;
+        p.biast_bytes = round256((size_t)H * (p.SkA + 1) * p.SqB * sizeof(float));
+        p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
+        return p;
+    }
     // row groups of the dK/dV kernel: at most the query tiles of a window, which they walk from
     // staggered starts; the most row groups (waves per CU) first, then the fewest windows
-    const int64_t qtiles = std::max<int64_t>((Sq + 31) / 32, 1);
     int qg_max = p.DP == 32 ? 4 : 2;
     while (qg_max > qtiles) qg_max /= 2;
     p.QG = 0;
@@ -958,7 +1279,6 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     int per_cu = std::max(1, std::min(2048 / threads, (int)(limit / per_wg)));
     const int64_t slots = (int64_t)cu_count(device) * per_cu;
     const int64_t cols = std::max<int64_t>(H * p.kblocks * p.windows, 1);
-    const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
     int64_t best = 1, best_cost = INT64_MAX;
     for (int64_t ch = 1; ch <= Nr; ++ch) {
         // rows per workgroup, a whole number of passes of its QG row groups where N allows
@@ -977,7 +1297,8 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.chunk = (int)((Nr + best - 1) / best);
     p.chunks = (int)((N + p.chunk - 1) / p.chunk);
     p.delta_bytes = round256((size_t)N * H * p.SqA * sizeof(float));  // half of the query terms
-    p.biast_bytes = round256((size_t)H * p.SkA * p.SqA * sizeof(half_t));
+    p.SqB = p.SqA;
+    p.biast_bytes = round256((size_t)H * (p.SkA + 1) * p.SqB * sizeof(float));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     p.dkv_bytes = p.windows > 1 ? round256((size_t)2 * p.windows * N * H * Sk * D * sizeof(float)) : 0;
     return p;
@@ -1014,12 +1335,26 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     const int64_t g1 = qt * a.H * a.N;
     if (g1 > INT32_MAX) return invalid("attention_bwd: too many work items");
     stage_mark(stream, 0);
-    const int64_t gb = (int64_t)(a.SqA / 32) * p.kblocks * a.H;
+    const int64_t gb = (int64_t)(a.SqB / 32) * p.kblocks * a.H;
     hipLaunchKernelGGL(attn_bwd_biast_kernel, dim3((unsigned)gb), dim3(256), 0, stream, a);
     stage_mark(stream, 1);
     hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
     stage_mark(stream, 2);
-    if (p.QG == 4) {
+    if (p.QT > 0) {
+        if constexpr (DP == 32) {
+            const int64_t g2 = (int64_t)p.chunks * a.H * p.kblocks;
+#define CLK_DKDV_REG(QT_)                                                                        \
+    if (p.QT == QT_) {                                                                           \
+        if (want_dbias) {                                                                        \
+            hipLaunchKernelGGL((attn_bwd_dkdv_reg_kernel<QT_, true>), dim3((unsigned)g2), dim3(512), 0, stream, a); \
+        } else {                                                                                 \
+            hipLaunchKernelGGL((attn_bwd_dkdv_reg_kernel<QT_, false>), dim3((unsigned)g2), dim3(512), 0, stream, a); \
+        }                                                                                        \
+    }
+            CLK_DKDV_REG(4) CLK_DKDV_REG(8) CLK_DKDV_REG(12)
+#undef CLK_DKDV_REG
+        }
+    } else if (p.QG == 4) {
         if constexpr (DP == 32) launch_dkdv<DP, 4>(stream, a, p, want_dbias);
     } else if (p.QG == 2) {
         launch_dkdv<DP, 2>(stream, a, p, want_dbias);
@@ -1065,8 +1400,9 @@ extern "C" int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int6
     }
     if (plan == nullptr || count < 0) return invalid("attention_bwd_plan: no output array");
     const BwdPlan p = plan_bwd(device, N, H, Sq, Sk, D);
-    const int64_t vals[] = {p.QG, p.chunk, p.chunks, (p.chunk + p.QG - 1) / p.QG, p.windows};
-    for (int i = 0; i < count && i < 5; ++i) plan[i] = vals[i];
+    const int64_t vals[] = {p.QG, p.chunk, p.chunks, (p.chunk + p.QG - 1) / p.QG, p.windows,
+                            p.QT > 0 ? 1 : 0};
+    for (int i = 0; i < count && i < 6; ++i) plan[i] = vals[i];
     return ok();
 }
 
@@ -1175,11 +1511,12 @@ static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffe
     a.dbias = static_cast<float*>(dbias->data);
     char* ws = static_cast<char*>(workspace);
     a.qstat = reinterpret_cast<float*>(ws);
-    a.biast = reinterpret_cast<half_t*>(ws + 2 * p.delta_bytes);
+    a.biast = reinterpret_cast<float*>(ws + 2 * p.delta_bytes);
     a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
     a.dkv = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
     a.SqA = p.SqA;
+    a.SqB = p.SqB;
     a.SkA = p.SkA;
     a.kblocks = p.kblocks;
     a.chunk = p.chunk;

@@ -18,6 +18,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float8v __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
 
@@ -25,6 +26,7 @@ constexpr int kWave = 64;
 // -inf would leave inf - inf on a row whose keys are all masked (cuda/volta_attn.h:9-11).
 constexpr float kMaskedLogit = -1.0e4f;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kMaskedLogit2 = kMaskedLogit * kLog2e;  // in the exp2 domain
 
 // One v_mfma_f32_16x16x32_f16: D[16x16] += A[16x32] B[32x16], fp32 accumulate. Lane l supplies
 // A row (l % 16) and B column (l % 16), eight contraction slots each (slot group l / 16), and

@@ -113,7 +113,8 @@ size_t clk_attention_bwd_noalloc_scratch_size(void);
 
 /* Diagnostic, no counterpart in the reference: the backward's launch plan for these shapes on
  * this device, plan[0..count) = {row groups per dK/dV workgroup, batch rows per workgroup
- * (chunk), chunks, row passes per workgroup, query windows}. */
+ * (chunk), chunks, row passes per workgroup, query windows, 1 where the dK/dV kernel keeps its
+ * dBias partial in registers (D <= 32, Sq <= 384) else 0}. */
 int clk_attention_bwd_plan(int32_t device, int64_t N, int64_t H, int64_t Sq, int64_t Sk,
                            int64_t D, int64_t* plan, int32_t count);
 
