@@ -984,7 +984,7 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
                 }
                 if constexpr (DBIAS) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) dbias[u][j] += dsf[j];
+                    for (int j = 0; j < 8; ++j) dbias[u][j] = pin_f32(dbias[u][j] + dsf[j]);  // here
                 }
                 // dV^T += dO^T P, dK^T += Q^T dS (k-slots queries 8 g + j, read transposed)
 #pragma unroll

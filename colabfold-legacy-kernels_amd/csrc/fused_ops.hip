@@ -1257,13 +1257,15 @@ void epilogue_kernel(EpiArgs a) {
 //
 // out^T = W2^T relu(W1 X^T + b1) + b2 over hidden chunks of 64: the first product's accumulator
 // (rows = hidden units in pair order) is exactly the B operand of the second, so the hidden
-// activation never leaves registers. Weight chunks stream through LDS; a 128-row tile (32 rows a
-// wave) amortises each chunk over 64 MFMAs per wave. The biases live in LDS, so no global load is
-// waited for between a chunk's prefetch and its use; the last chunk prefetches the first for the
-// next tile, and at C <= 128 (where registers allow) the next tile's rows are fetched during this
-// tile's chunks.
+// activation never leaves registers. Weight chunks stream through LDS and every weight fragment a
+// wave reads feeds one MFMA per 16-row block of its rows: at C = 128 a 256-row tile (two blocks a
+// wave, which halves the LDS weight reads per MFMA: the kernel is bound by them), otherwise 128
+// rows. The biases live in LDS, so no global load is waited for between a chunk's prefetch and
+// its use; the last chunk prefetches the first for the next tile, and at C = 64 (where registers
+// allow) the next tile's rows are fetched during this tile's chunks.
 constexpr int kHid = 64;
-constexpr int kTransRows = 128;
+template <int C>
+constexpr int trans_rows() { return C == 128 ? 256 : 128; }
 
 struct TransArgs {
     const half_t* x;
@@ -1285,9 +1287,9 @@ struct TransTile {
     static constexpr int kSub = C > 128 ? 32 : 64;        // keep granularity (volta_ops.cu:551-553)
 };
 
-// Threads per workgroup: at C <= 128 eight waves of one 16-row block each (more waves per SIMD to
-// hide each other's LDS and MFMA latency than four waves of two row blocks allow: two instead of
-// one at C = 128, four instead of two at C = 64), at C = 256 four waves of two row blocks.
+// Threads per workgroup: at C <= 128 eight waves (of two 16-row blocks each at C = 128, of one at
+// C = 64, where more waves per SIMD hide each other's LDS and MFMA latency better), at C = 256
+// four waves of two row blocks.
 // Workgroups per CU the kernel is compiled for: two at C = 64.
 constexpr int trans_threads(int C) { return C <= 128 ? 512 : 256; }
 constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
@@ -1295,13 +1297,14 @@ constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
 template <int C, bool ADD, int TH, bool BF>
 __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_kernel(TransArgs a) {
     using T = TransTile<C>;
-    constexpr int TW = TH / kWave, RB = kTransRows / 16 / TW, kCPT = T::kChunks / TH;
-    static_assert(RB * TW * 16 == kTransRows && kCPT * TH == T::kChunks, "whole row blocks and chunks");
-    constexpr int KS = T::KS, NCB = C / 16, NSUB = kTransRows / T::kSub;
-    constexpr bool PF = C <= 128;
+    constexpr int kTR = trans_rows<C>();
+    constexpr int TW = TH / kWave, RB = kTR / 16 / TW, kCPT = T::kChunks / TH;
+    static_assert(RB * TW * 16 == kTR && kCPT * TH == T::kChunks, "whole row blocks and chunks");
+    constexpr int KS = T::KS, NCB = C / 16, NSUB = kTR / T::kSub;
+    constexpr bool PF = C == 64;
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     half_t* Xf = lds;                          // 8 row blocks
-    half_t* W1 = Xf + kTransRows * C;          // hidden chunk of w1, then of w2
+    half_t* W1 = Xf + kTR * C;          // hidden chunk of w1, then of w2
     half_t* W2 = W1 + T::kW1;
     float* sc = reinterpret_cast<float*>(W2 + T::kW2);
     float* of = sc + C;
@@ -1315,7 +1318,7 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
     for (int i = threadIdx.x; i < a.H; i += TH) b1s[i] = a.b1[i];
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int r16 = lane & 15, g = lane >> 4;
-    const int tiles = (a.M + kTransRows - 1) / kTransRows;
+    const int tiles = (a.M + kTR - 1) / kTR;
     const int chunks = a.H / kHid;
 
     // weight chunk j: W1 fragments of hidden rows 64 j + pair_row(hb, r), W2 fragments of output
@@ -1343,11 +1346,11 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
         for (int u = 0; u < kCPT; ++u) fst8(W1 + (threadIdx.x + u * TH) * 8, wreg[u]);
     };
 
-    RowTile<C, kTransRows, TH> xt;
+    RowTile<C, kTR, TH> xt;
     fetch_w(0);
-    if (PF && blockIdx.x < tiles) fetch_rows<C, kTransRows>(xt, a.x, a.M, blockIdx.x * kTransRows);
+    if (PF && blockIdx.x < tiles) fetch_rows<C, kTR>(xt, a.x, a.M, blockIdx.x * kTR);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-        const int m0 = tile * kTransRows;
+        const int m0 = tile * kTR;
         int work[NSUB];
         bool any = false;
 #pragma unroll
@@ -1357,19 +1360,19 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
         }
         if (!any) {
             if (!ADD) {
-                for (int i = threadIdx.x; i < kTransRows * C / 8; i += TH) {
+                for (int i = threadIdx.x; i < kTR * C / 8; i += TH) {
                     const int r = i / (C / 8), c = (i % (C / 8)) * 8;
                     if (work[r / T::kSub] == kPadding && m0 + r < a.M)
                         fst8(a.out + (int64_t)(m0 + r) * C + c, fzero8());
                 }
             }
             if (PF && tile + (int)gridDim.x < tiles)
-                fetch_rows<C, kTransRows>(xt, a.x, a.M, (tile + gridDim.x) * kTransRows);
+                fetch_rows<C, kTR>(xt, a.x, a.M, (tile + gridDim.x) * kTR);
             continue;
         }
-        if (!PF) fetch_rows<C, kTransRows>(xt, a.x, a.M, m0);
+        if (!PF) fetch_rows<C, kTR>(xt, a.x, a.M, m0);
         __syncthreads();
-        ln_rows_to_frags<C, kTransRows, false, true, TH, BF>(Xf, xt, sc, of, a.eps);
+        ln_rows_to_frags<C, kTR, false, true, TH, BF>(Xf, xt, sc, of, a.eps);
 
         float4v acc[NCB][RB];
 #pragma unroll
@@ -1388,7 +1391,7 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
                     for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(RB * wave + rb, ks, KS, lane));
                 // issued before the weights, so waiting for those (in issue order) covers these
                 if (PF && tile + (int)gridDim.x < tiles)
-                    fetch_rows<C, kTransRows>(xt, a.x, a.M, (tile + gridDim.x) * kTransRows);
+                    fetch_rows<C, kTR>(xt, a.x, a.M, (tile + gridDim.x) * kTR);
             }
             fetch_w(j + 1 < chunks ? j + 1 : 0);  // the first chunk again for the next tile
 
@@ -1822,8 +1825,9 @@ template <int C, bool ADD, bool BF>
 static int run_transition(const TransArgs& a, hipStream_t s) {
     using T = TransTile<C>;
     constexpr int TH = trans_threads(C);
-    const size_t lds = (size_t)(kTransRows * C + T::kW1 + T::kW2) * 2 + (size_t)(3 * C + a.H) * 4;
-    const int64_t tiles = (a.M + kTransRows - 1) / kTransRows;
+    constexpr int kTR = trans_rows<C>();
+    const size_t lds = (size_t)(kTR * C + T::kW1 + T::kW2) * 2 + (size_t)(3 * C + a.H) * 4;
+    const int64_t tiles = (a.M + kTR - 1) / kTR;
     const dim3 grid(persistent_grid(tiles, lds, trans_per_cu(C)));
     if (int st = launch_fused("transition", transition_kernel<C, ADD, TH, BF>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
