@@ -4,8 +4,9 @@
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-fused] [--no-packed]
                   [--no-extra] [--calibration-copy MIB]
   python bench.py --stats-summary DIR            (text summary of a rocprofv3 --stats run)
-  python bench.py --traffic-summary FETCH_DIR WRITE_DIR [--calibration-copy MIB]
+  python bench.py --traffic-summary FETCH_DIR WRITE_DIR [--calibration-copy MIB] [--prefix c2:]
                                                  (HBM bytes per dispatch from two --pmc runs)
+  python bench.py --only c2|c5 ...                (profiling: that config's object alone)
   python bench.py --counter-summary DIR [DIR ...] (per-kernel means of the counters of --pmc runs)
 
 A step is one attention forward + backward of BASELINE config C3 (MSA row attention with pair
@@ -17,7 +18,8 @@ objects of the same line: "c2" (triangle attention fwd + bwd, N_res = 256) and "
 attention forward, N_res = 1024, want_lse off), each with its kernels and roofline. Per-kernel durations come from HIP events that the library records
 on its launch stream at its kernel boundaries (clk_set_stage_events); the roofline object is the
 dominant kernel's, its "traffic" the HBM bytes per dispatch that the committed rocprofv3 counter
-summary (profiles/attention_c3_traffic.txt) measured for that kernel. Reported beside the step:
+summaries (profiles/attention_c3_traffic.txt, profiles/attention_c2_c5_traffic.txt) measured for
+that kernel at that config. Reported beside the step:
 the gated packed forward VoltaMmaPacked (G = 4) on the same shape, and the fused pair-stack ops
 of config C4 (M = 262144 rows, c = 64 and 128), the unfused LayerNorm and gated dual projection
 at c = 128 on the same rows, and the outer product mean pair on C3's residues (B = D = 384, 16 MSA
@@ -48,6 +50,8 @@ PEAK_TFLOPS = 2516.6   # MI355X dense fp16 MFMA (256 CU x 2.4 GHz x 4096 flop/cl
 PEAK_GBS = 8000.0      # MI355X HBM3E
 MALL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_c3_traffic.txt")
+# C2's and C5's kernels, with stage names prefixed "c2:" / "c5:"
+EXTRA_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attention_c2_c5_traffic.txt")
 
 N, H, S, D = 512, 8, 384, 32
 FWD_STAGES = ("attn_fwd",)
@@ -55,6 +59,7 @@ BWD_STAGES = ("bwd_biast", "bwd_dq", "bwd_dkdv", "bwd_dbias")
 # kernel-name fragment in a rocprofv3 record -> the bench's stage name
 KERNEL_STAGES = (("attn_fwd_kernel", "attn_fwd"), ("attn_bwd_biast_kernel", "bwd_biast"),
                  ("attn_bwd_dq_kernel", "bwd_dq"), ("attn_bwd_dkdv_kernel", "bwd_dkdv"),
+                 ("attn_bwd_dkdv_reg_kernel", "bwd_dkdv"), ("attn_bwd_dkdv_sum_kernel", "bwd_dkdv_sum"),
                  ("attn_bwd_dbias_kernel", "bwd_dbias"))
 CALIBRATION_KERNEL = "bitwise_not"
 
@@ -122,8 +127,13 @@ def attention_algo(ws_bytes, n=N, h=H, s=S, d=D):
     row = n * h * s * 4                     # one fp32 [N,H,S] row statistic
     bias, km, dbias = h * s * s * 2, n * s, h * s * s * 4
     sqa, ska = -(-s // 32) * 32, -(-s // 64) * 64
-    biast = h * ska * sqa * 2
-    partial = max(ws_bytes - 2 * row - biast, 0)
+    # the workspace: two query-term rows, the transposed log2e bias (fp32, one masked-logit row
+    # per head, queries padded to 32 QT where the register dK/dV kernel runs), the dBias partials
+    r256 = lambda b: -(-b // 256) * 256
+    qt = sqa // 32
+    sqb = 32 * (4 if qt <= 4 else 8 if qt <= 8 else 12) if d == 32 and qt <= 12 else sqa
+    biast = h * (ska + 1) * sqb * 4
+    partial = max(ws_bytes - 2 * r256(n * h * sqa * 4) - r256(biast), 0)
     return {
         "attn_fwd": (4 * u, 3 * t + bias + km + t + row, 0),
         "bwd_biast": (0.0, bias + biast, 0),
@@ -219,8 +229,9 @@ def bench_attention(torch, hip, steps, warmup, ev, n=N, h=H, s=S, d=D, mask_frac
     return total_ms / steps, (14 if backward else 4) * u, kernels
 
 
-def roofline_of(kernels):
-    """The roofline object of the dominant (longest) kernel of a step."""
+def roofline_of(kernels, prefix=""):
+    """The roofline object of the dominant (longest) kernel of a step; `prefix` names the config
+    whose profiled traffic applies ("" for C3, "c2:" or "c5:")."""
     dom = max(kernels, key=lambda k: kernels[k]["ms"])
     kd = kernels[dom]
     if kd["bound"] == "mfma":
@@ -228,7 +239,7 @@ def roofline_of(kernels):
     else:
         roof = {"bound": "hbm", "achieved": kd["gbs"], "peak": PEAK_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 4)
-    roof["traffic"] = load_traffic(dom)
+    roof["traffic"] = load_traffic(prefix + dom)
     roof["kernel"] = dom
     roof["ms"] = kd["ms"]
     return roof
@@ -255,7 +266,7 @@ def bench_extra(torch, hip, ev, name, steps, warmup):
     return {"workload": workload, "shape": [cfg["n"], cfg["h"], cfg["s"], cfg["d"]],
             "ms_per_step": round(ms, 5), "tflops": round(flops / ms / 1e9, 2),
             "frac_mfma_step": round(t_mfma / ms, 4), "flops_per_step": flops,
-            "roofline": roofline_of(kernels), "kernels": kernels}
+            "roofline": roofline_of(kernels, name + ":"), "kernels": kernels}
 
 
 def bench_packed(torch, hip, iters, warmup, ev):
@@ -514,9 +525,9 @@ def _counter_means(d, counter):
     return {name: statistics.mean(v) for name, v in out.items()}
 
 
-def traffic_summary(fetch_dir, write_dir, mib):
+def traffic_summary(fetch_dir, write_dir, mib, prefix=""):
     """HBM bytes per dispatch: FETCH_SIZE and WRITE_SIZE (KiB) scaled by what the same counters
-    read for the calibration copy of known size."""
+    read for the calibration copy of known size; attention stages are named prefix + stage."""
     fetch, write = _counter_means(fetch_dir, "FETCH_SIZE"), _counter_means(write_dir, "WRITE_SIZE")
     cal = [n for n in fetch if CALIBRATION_KERNEL in n]
     if not cal or not any(CALIBRATION_KERNEL in n for n in write):
@@ -534,7 +545,8 @@ def traffic_summary(fetch_dir, write_dir, mib):
         short = name.replace("void ", "").replace("clk::", "").split("(")[0].replace(" ", "")
         by = (fetch[name] * f_fetch + write[name] * f_write) * 1024
         lines.append("%s %s fetch_kib %.0f write_kib %.0f traffic_bytes %.0f"
-                     % ("kernel" if stage else "fused", stage or short, fetch[name], write[name], by)
+                     % ("kernel" if stage else "fused", prefix + stage if stage else short,
+                        fetch[name], write[name], by)
                      + ("  (%s)" % short if stage else ""))
     return "\n".join(lines)
 
@@ -568,14 +580,16 @@ def counter_summary(dirs):
 
 
 def load_traffic(stage):
-    """HBM bytes per dispatch of `stage` from the committed counter summary, or None."""
-    try:
-        for line in open(TRAFFIC_FILE):
-            t = line.split()
-            if len(t) >= 8 and t[0] == "kernel" and t[1] == stage and t[6] == "traffic_bytes":
-                return float(t[7])
-    except OSError:
-        return None
+    """HBM bytes per dispatch of `stage` (C3's, or "c2:..." / "c5:...") from the committed counter
+    summaries, or None."""
+    for path in (TRAFFIC_FILE, EXTRA_TRAFFIC_FILE):
+        try:
+            for line in open(path):
+                t = line.split()
+                if len(t) >= 8 and t[0] == "kernel" and t[1] == stage and t[6] == "traffic_bytes":
+                    return float(t[7])
+        except OSError:
+            continue
     return None
 
 
@@ -589,6 +603,9 @@ def main():
     ap.add_argument("--no-packed", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C2 and C5 configs")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB")
+    ap.add_argument("--only", choices=sorted(EXTRA_CONFIGS), metavar="CONFIG",
+                    help="profiling: run only this extra config (c2 or c5) and print its object")
+    ap.add_argument("--prefix", default="", help="stage-name prefix for --traffic-summary")
     ap.add_argument("--stats-summary", metavar="DIR")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--counter-summary", nargs="+", metavar="DIR")
@@ -597,7 +614,8 @@ def main():
         print(stats_summary(args.stats_summary))
         return
     if args.traffic_summary:
-        print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.calibration_copy or 256))
+        print(traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.calibration_copy or 256,
+                              args.prefix))
         return
     if args.counter_summary:
         print(counter_summary(args.counter_summary))
@@ -616,6 +634,10 @@ def main():
     ev = HipEvents()
     if args.calibration_copy:
         calibration_copy(torch, args.calibration_copy)
+    if args.only:
+        print(json.dumps({args.only: bench_extra(torch, hip, ev, args.only, args.steps, args.warmup)}),
+              flush=True)
+        return
     ms_step, flops_step, kernels = bench_attention(torch, hip, args.steps, args.warmup, ev)
     roof = roofline_of(kernels)
     line = {
