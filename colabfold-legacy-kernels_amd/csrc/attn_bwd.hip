@@ -949,50 +949,59 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
             stage(par ^ 1);
             fetch_s(pass + (st + 2) / kSteps, (st + 2) % kSteps);
             const half_t* buf = lds + par * kBuf + qh * 2 * kSub;
+            // the step's two tiles phase by phase, so each phase has two independent chains
+            float x[2][8];
+            float4v dp[2][2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int u = 2 * st + i;  // tile within the half
+                const int u = 2 * st + i;
                 const half_t* Qs = buf + i * kSub;
                 const half_t* Os = Qs + kOs;
                 const int qo = par * 256 + 64 * i;
-                // S from -lse2 / c1 and dP from -delta: the lane holds queries 8 g + 4 qb + i4
-                float x[8];
-                float4v dp[2];
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb) {
                     float4v sacc = *reinterpret_cast<const float4v*>(qtS + qo + 4 * qb);
-                    dp[qb] = *reinterpret_cast<const float4v*>(qtD + qo + 4 * qb);
+                    dp[i][qb] = *reinterpret_cast<const float4v*>(qtD + qo + 4 * qb);
                     const int w = 2 * reg_word(16 * qb + r16, 8 * g);
                     const half8 qa = *reinterpret_cast<const half8*>(Qs + w);
                     const half8 oa = *reinterpret_cast<const half8*>(Os + w);
                     sacc = mfma16x16x32(qa, kop, sacc);
-                    dp[qb] = mfma16x16x32(oa, vop, dp[qb]);
+                    dp[i][qb] = mfma16x16x32(oa, vop, dp[i][qb]);
                     const float4 bb = *reinterpret_cast<const float4*>(brow + 32 * u + 4 * qb);
-                    x[4 * qb + 0] = fmaf(sacc[0], c1, bb.x);
-                    x[4 * qb + 1] = fmaf(sacc[1], c1, bb.y);
-                    x[4 * qb + 2] = fmaf(sacc[2], c1, bb.z);
-                    x[4 * qb + 3] = fmaf(sacc[3], c1, bb.w);
+                    x[i][4 * qb + 0] = fmaf(sacc[0], c1, bb.x);
+                    x[i][4 * qb + 1] = fmaf(sacc[1], c1, bb.y);
+                    x[i][4 * qb + 2] = fmaf(sacc[2], c1, bb.z);
+                    x[i][4 * qb + 3] = fmaf(sacc[3], c1, bb.w);
                 }
-                half8 pb, dsb;
-                float dsf[8];
+            }
+            half8 pb[2], dsb[2];
+            float dsf[2][8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = exp2_fast(x[j]);
-                    dsf[j] = pin_f32(p * dp[j >> 2][j & 3]);
-                    pb[j] = (half_t)p;
-                    dsb[j] = (half_t)dsf[j];
-                }
-                if constexpr (DBIAS) {
+            for (int j = 0; j < 8; ++j)
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) dbias[u][j] = pin_f32(dbias[u][j] + dsf[j]);  // here
+                for (int i = 0; i < 2; ++i) {
+                    const float p = exp2_fast(x[i][j]);
+                    dsf[i][j] = pin_f32(p * dp[i][j >> 2][j & 3]);
+                    pb[i][j] = (half_t)p;
+                    dsb[i][j] = (half_t)dsf[i][j];
                 }
-                // dV^T += dO^T P, dK^T += Q^T dS (k-slots queries 8 g + j, read transposed)
+            if constexpr (DBIAS) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) dbias[2 * st + i][j] = pin_f32(dbias[2 * st + i][j] + dsf[i][j]);
+            }
+            // dV^T += dO^T P, dK^T += Q^T dS (k-slots queries 8 g + j, read transposed)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const half_t* Qs = buf + i * kSub;
+                const half_t* Os = Qs + kOs;
 #pragma unroll
                 for (int db = 0; db < 2; ++db) {
                     const half8 ot = reg_operand_tr(Os, g, r16, db);
                     const half8 qt = reg_operand_tr(Qs, g, r16, db);
-                    accv[db] = mfma16x16x32(ot, pb, accv[db]);
-                    acck[db] = mfma16x16x32(qt, dsb, acck[db]);
+                    accv[db] = mfma16x16x32(ot, pb[i], accv[db]);
+                    acck[db] = mfma16x16x32(qt, dsb[i], acck[db]);
                 }
             }
             if (st == kSteps - 1 && qh == 1) {
