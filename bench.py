@@ -59,7 +59,8 @@ BWD_STAGES = ("bwd_biast", "bwd_dq", "bwd_dkdv", "bwd_dbias")
 # kernel-name fragment in a rocprofv3 record -> the bench's stage name
 KERNEL_STAGES = (("attn_fwd_kernel", "attn_fwd"), ("attn_bwd_biast_kernel", "bwd_biast"),
                  ("attn_bwd_dq_kernel", "bwd_dq"), ("attn_bwd_dkdv_kernel", "bwd_dkdv"),
-                 ("attn_bwd_dkdv_reg_kernel", "bwd_dkdv"), ("attn_bwd_dkdv_sum_kernel", "bwd_dkdv_sum"),
+                 ("attn_bwd_dkdv_reg_kernel", "bwd_dkdv"), ("attn_bwd_dkdv_reg3_kernel", "bwd_dkdv"),
+                 ("attn_bwd_dkdv_sum_kernel", "bwd_dkdv_sum"),
                  ("attn_bwd_dbias_kernel", "bwd_dbias"))
 CALIBRATION_KERNEL = "bitwise_not"
 

@@ -1050,6 +1050,259 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// The register dK/dV kernel for QT = 12 (256 < Sq <= 384, D = 32) at three waves per SIMD:
+// twelve waves per workgroup, key group w % 4 by query third w / 4 (four tiles each), so the
+// dBias partial is 32 registers per lane and the kernel fits 168 VGPRs. Its LDS holds the
+// workgroup's bias as fp16 (the original values, recovered exactly from the fp32 log2e form), so
+// s2 = log2e (scale S + bias) takes an fma with the fp16 operand read in place and a multiply.
+// The thirds' dK / dV sums meet in LDS once per row, thirds 1 and 2 into third 0 in that order.
+// Everything else is attn_bwd_dkdv_reg_kernel's.
+// ------------------------------------------------------------------------------------------
+template <bool DBIAS>
+__global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
+    constexpr int DP = 32, QT = 12, TT = 4;  // tiles per third
+    constexpr int kSteps = TT / 2;
+    constexpr int kTile = 32 * DP, kOs = kTile + 64, kSub = kOs + kTile;
+    constexpr int kBuf = 6 * kSub;           // halfs of a step: [third][tile]
+    constexpr int SqB = 32 * QT;
+    constexpr int kBRow = SqB + 8;           // LDS bias row stride (halfs)
+    __shared__ __attribute__((aligned(16))) half_t bias_l[65 * kBRow];  // rows: 64 keys, masked
+    __shared__ __attribute__((aligned(16))) half_t lds[2 * kBuf];
+    // query terms [buf][third][tile][-lse2 / c1 x 32, -delta x 32], then 768 zeros
+    __shared__ __attribute__((aligned(16))) float qterms[2 * 384 + 768];
+    // thirds 1 and 2's dK / dV sums of a row: [third - 1][key group][float4 j][lane]
+    __shared__ __attribute__((aligned(16))) float4 red[2 * 4 * 4 * 64];
+
+    const int item = xcd_item(blockIdx.x, gridDim.x);
+    const int kblk = item % a.kblocks, rest = item / a.kblocks;
+    const int c = rest % a.chunks, h = rest / a.chunks;
+    const int n_begin = c * a.chunk;
+    const int rows = min(a.N, n_begin + a.chunk) - n_begin;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int kg = wave & 3, q3 = wave >> 2;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int klocal = kg * 16 + r16;
+    const int key = kblk * 64 + klocal;
+    const bool kin = key < a.Sk;
+    const float c1s = a.c1s;
+
+    // the workgroup's bias, fp16: rows kblk 64 .. + 63 and the masked-logit row SkA
+    {
+        constexpr int kFill = (65 * (SqB / 4) + 767) / 768;
+        const float* src = a.biast + (int64_t)h * (a.SkA + 1) * SqB;
+#pragma unroll
+        for (int f = 0; f < kFill; ++f) {
+            const int idx = tid + 768 * f;
+            if (idx < 65 * (SqB / 4)) {
+                const int r = idx / (SqB / 4), c4 = idx - r * (SqB / 4);
+                const int srow = r < 64 ? kblk * 64 + r : a.SkA;
+                const float4 v = *reinterpret_cast<const float4*>(src + (int64_t)srow * SqB + 4 * c4);
+                *reinterpret_cast<half4*>(bias_l + r * kBRow + 4 * c4) =
+                    half4{(half_t)(v.x * (1.f / kLog2e)), (half_t)(v.y * (1.f / kLog2e)),
+                          (half_t)(v.z * (1.f / kLog2e)), (half_t)(v.w * (1.f / kLog2e))};
+            }
+        }
+    }
+    if (tid < 192) reinterpret_cast<float4*>(qterms + 768)[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // this wave's staging share of a step: tile (third sq3, tile si) of tensor (Q, dO)
+    const int ti = wave >> 1, tensor = wave & 1, sq3 = ti >> 1, si = ti & 1;
+    const int crow = lane >> 2, ccol = (lane & 3) * 8;
+    const uint32_t cvoff = (uint32_t)((crow * DP + ccol) * 2);
+    const int cdst0 = (2 * sq3 + si) * kSub + tensor * kOs + 2 * reg_word(perm_row(crow, 8), ccol);
+    const int cdst1 = (2 * sq3 + si) * kSub + tensor * kOs + 2 * reg_word(perm_row(crow + 16, 8), ccol);
+    const half_t* const csrc = tensor ? a.dout : a.q;
+    // waves 0 and 1 stage the query terms: flat lane L < 96, tile L / 16 of [third][tile]
+    const int qL = wave * kWave + lane;
+    const int qt_t = qL >> 4;
+    const uint32_t qt_f = (uint32_t)(4 * (qL & 15));
+
+    const auto row_nh = [&](int pass) -> int64_t {
+        return (int64_t)(n_begin + (pass < rows ? pass : 0)) * a.H + h;
+    };
+    half8 chk[2];
+    float4 qst;
+    const auto fetch_s = [&](int pass, int step) {
+        const int64_t nh = row_nh(pass);
+        const int q0 = 32 * (sq3 * TT + 2 * step + si);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<half_t*>(csrc + (nh * a.Sq + q0) * DP), 0, max(a.Sq - q0, 0) * DP * 2, 0x00020000);
+        chk[0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff, 0, 0));
+        chk[1] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff + 16u * DP * 2u, 0, 0));
+        if (wave < 2) {
+            const int tg = (qt_t >> 1) * TT + 2 * step + (qt_t & 1);
+            const auto rq = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(a.qstat + nh * a.SqA * 2), 0, a.SqA * 2 * 4, 0x00020000);
+            qst = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                rq, qL < 96 ? ((uint32_t)(64 * tg) + qt_f) * 4u : 0x80000000u, 0, 0));
+        }
+    };
+    const auto stage = [&](int buf) {
+        half_t* dst = lds + buf * kBuf;
+        *reinterpret_cast<half8*>(dst + cdst0) = chk[0];
+        *reinterpret_cast<half8*>(dst + cdst1) = chk[1];
+        if (wave < 2 && qL < 96) *reinterpret_cast<float4*>(qterms + buf * 384 + 4 * qL) = qst;
+    };
+
+    half8 kopn, vopn;
+    uint32_t mbn = 0u;
+    const auto fetch_kv = [&](int pass) {
+        const int64_t nh = row_nh(pass);
+        const int kc = kin ? key : 0;
+        mbn = (uint32_t)a.kmask[(nh / a.H) * a.Sk + kc];
+        const int64_t off = (nh * a.Sk + kc) * DP + 8 * g;
+        kopn = bld8(a.k + off);
+        vopn = bld8(a.v + off);
+    };
+
+    float dbias[TT][8];
+    if constexpr (DBIAS) {
+#pragma unroll
+        for (int u = 0; u < TT; ++u)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dbias[u][j] = 0.f;
+    }
+
+    if (rows > 0) {
+        fetch_kv(0);
+        fetch_s(0, 0);
+        stage(0);
+        fetch_s(0, 1);
+    }
+    __syncthreads();
+
+    for (int pass = 0; pass < rows; ++pass) {
+        const int n = n_begin + pass;
+        const bool alive = kin && mbn != 0u;
+        const half8 kop = alive && a.kscale ? kopn : bzero8();
+        const half8 vop = alive ? vopn : bzero8();
+        // a dead key's lane: the masked-logit bias row, and -delta from the zeroed area
+        const half_t* const brow = bias_l + (alive ? klocal : 64) * kBRow + q3 * TT * 32 + 8 * g;
+        const float* const qtS = qterms + q3 * 128 + 8 * g;
+        const float* const qtD = qtS + 32 + (alive ? 0 : 768);
+        float4v accv[2], acck[2];
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+            accv[db] = float4v{0.f, 0.f, 0.f, 0.f};
+            acck[db] = float4v{0.f, 0.f, 0.f, 0.f};
+        }
+        fetch_kv(pass + 1);
+
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            const int par = st & 1;  // kSteps is even
+            stage(par ^ 1);
+            fetch_s(pass + (st + 2) / kSteps, (st + 2) % kSteps);
+            const half_t* buf = lds + par * kBuf + q3 * 2 * kSub;
+            float x[2][8];
+            float4v dp[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int u = 2 * st + i;
+                const half_t* Qs = buf + i * kSub;
+                const half_t* Os = Qs + kOs;
+                const int qo = par * 384 + 64 * i;
+                const half8 bb = *reinterpret_cast<const half8*>(brow + 32 * u);
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    float4v sacc = *reinterpret_cast<const float4v*>(qtS + qo + 4 * qb);
+                    dp[i][qb] = *reinterpret_cast<const float4v*>(qtD + qo + 4 * qb);
+                    const int w = 2 * reg_word(16 * qb + r16, 8 * g);
+                    const half8 qa = *reinterpret_cast<const half8*>(Qs + w);
+                    const half8 oa = *reinterpret_cast<const half8*>(Os + w);
+                    sacc = mfma16x16x32(qa, kop, sacc);
+                    dp[i][qb] = mfma16x16x32(oa, vop, dp[i][qb]);
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        x[i][4 * qb + i4] = fmaf(sacc[i4], c1s, (float)bb[4 * qb + i4]) * kLog2e;
+                }
+            }
+            half8 pb[2], dsb[2];
+            float dsf[2][8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const float p = exp2_fast(x[i][j]);
+                    dsf[i][j] = pin_f32(p * dp[i][j >> 2][j & 3]);
+                    pb[i][j] = (half_t)p;
+                    dsb[i][j] = (half_t)dsf[i][j];
+                }
+            if constexpr (DBIAS) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) dbias[2 * st + i][j] = pin_f32(dbias[2 * st + i][j] + dsf[i][j]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const half_t* Qs = buf + i * kSub;
+                const half_t* Os = Qs + kOs;
+#pragma unroll
+                for (int db = 0; db < 2; ++db) {
+                    const half8 ot = reg_operand_tr(Os, g, r16, db);
+                    const half8 qt = reg_operand_tr(Qs, g, r16, db);
+                    accv[db] = mfma16x16x32(ot, pb[i], accv[db]);
+                    acck[db] = mfma16x16x32(qt, dsb[i], acck[db]);
+                }
+            }
+            if (st == kSteps - 1 && q3 > 0) {
+                float4* r = red + ((q3 - 1) * 4 + kg) * 4 * 64 + lane;
+                r[0] = make_float4(acck[0][0], acck[0][1], acck[0][2], acck[0][3]);
+                r[64] = make_float4(acck[1][0], acck[1][1], acck[1][2], acck[1][3]);
+                r[128] = make_float4(accv[0][0], accv[0][1], accv[0][2], accv[0][3]);
+                r[192] = make_float4(accv[1][0], accv[1][1], accv[1][2], accv[1][3]);
+            }
+            __syncthreads();
+        }
+
+        if (q3 == 0 && kin) {
+            // third 0 + third 1 + third 2, then lane holds d = 8 g .. + 8 of its key
+            float ks[8], vs[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ks[j] = acck[j / 4][j & 3];
+                vs[j] = accv[j / 4][j & 3];
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float4* r = red + (t * 4 + kg) * 4 * 64 + lane;
+                const float4 k0 = r[0], k1 = r[64], v0 = r[128], v1 = r[192];
+                ks[0] += k0.x; ks[1] += k0.y; ks[2] += k0.z; ks[3] += k0.w;
+                ks[4] += k1.x; ks[5] += k1.y; ks[6] += k1.z; ks[7] += k1.w;
+                vs[0] += v0.x; vs[1] += v0.y; vs[2] += v0.z; vs[3] += v0.w;
+                vs[4] += v1.x; vs[5] += v1.y; vs[6] += v1.z; vs[7] += v1.w;
+            }
+            const int64_t off = (((int64_t)n * a.H + h) * a.Sk + key) * DP + 8 * g;
+            half8 ok, ov;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                ok[j] = (half_t)(ks[j] * a.scale);
+                ov[j] = (half_t)vs[j];
+            }
+            *reinterpret_cast<half8*>(a.dk + off) = ok;
+            *reinterpret_cast<half8*>(a.dv + off) = ov;
+        }
+    }
+
+    if constexpr (DBIAS) {
+        const int qtiles = a.SqA / 32;
+        float* dst = a.partial + (((int64_t)c * a.H + h) * a.kblocks + kblk) * a.SqA * 64 + klocal;
+#pragma unroll
+        for (int u = 0; u < TT; ++u) {
+            const int ut = q3 * TT + u;
+            if (ut >= qtiles) continue;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dst[(int64_t)(32 * ut + 8 * g + j) * 64] = dbias[u][j];
+        }
+    }
+}
+
+template __global__ void attn_bwd_dkdv_reg3_kernel<true>(BwdArgs);
+template __global__ void attn_bwd_dkdv_reg3_kernel<false>(BwdArgs);
+
 // With more than one query window: dk = fp16(scale * sum of the windows' dK sums), dv = fp16(sum
 // of their dV sums), each summed in window order, four elements per thread (D % 4 == 0).
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_sum_kernel(BwdArgs a) {
@@ -1226,7 +1479,8 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     const int64_t qtiles = std::max<int64_t>((Sq + 31) / 32, 1);
     const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
     if (D == 32 && qtiles <= 12) {
-        // the register-partial kernel: one workgroup of eight waves per CU, one row per pass;
+        // the register-partial kernels: one workgroup of eight (QT 4, 8) or twelve (QT 12) waves
+        // per CU, one row per pass;
         // chunks trade rounds of workgroups against dbias partials to write and sum (one
         // partial weighs about H kblocks / 128 row passes)
         p.QT = qtiles <= 4 ? 4 : qtiles <= 8 ? 8 : 12;
@@ -1360,7 +1614,14 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
             hipLaunchKernelGGL((attn_bwd_dkdv_reg_kernel<QT_, false>), dim3((unsigned)g2), dim3(512), 0, stream, a); \
         }                                                                                        \
     }
-            CLK_DKDV_REG(4) CLK_DKDV_REG(8) CLK_DKDV_REG(12)
+            CLK_DKDV_REG(4) CLK_DKDV_REG(8)
+            if (p.QT == 12) {
+                if (want_dbias) {
+                    hipLaunchKernelGGL((attn_bwd_dkdv_reg3_kernel<true>), dim3((unsigned)g2), dim3(768), 0, stream, a);
+                } else {
+                    hipLaunchKernelGGL((attn_bwd_dkdv_reg3_kernel<false>), dim3((unsigned)g2), dim3(768), 0, stream, a);
+                }
+            }
 #undef CLK_DKDV_REG
         }
     } else if (p.QG == 4) {

@@ -129,13 +129,14 @@ def test_batch_sizes(hip, n):
 
 
 @pytest.mark.parametrize("n,h,s,registers", [(512, 8, 96, 1), (128, 16, 128, 1), (96, 4, 200, 1),
-                                              (256, 1, 416, 0), (256, 1, 448, 0)])
+                                              (64, 4, 300, 1), (256, 1, 416, 0), (256, 1, 448, 0)])
 def test_multi_pass_dkdv(hip, n, h, s, registers):
     """Shapes whose dK/dV workgroups take several passes over batch rows, so the row cursors
     roll over, the next row's K/V prefetch is used and the dBias partial accumulates across rows:
-    in registers (Sq <= 384 at D = 32: 96 with a ragged tile count, 128, and 200, whose query
-    tiles stop inside a 64-query step) or in LDS across row groups (416, 448). The results must
-    also repeat bit for bit."""
+    in registers (Sq <= 384 at D = 32: 96 with a ragged tile count, 128, 200, whose query
+    tiles stop inside a 64-query step, and 300, the twelve-wave kernel with padded tiles and a
+    ragged last chunk) or in LDS across row groups (416, 448). The results must also repeat bit
+    for bit."""
     plan = hip.attention_bwd_plan(n, h, s, s, 32)
     assert plan["passes"] > 1 and plan["registers"] == registers, plan
     got, ref = run(hip, n=n, h=h, sq=s, sk=s, d=32, seed=3)
