@@ -130,16 +130,18 @@ def attention_algo(ws_bytes, n=N, h=H, s=S, d=D):
     sqa, ska = -(-s // 32) * 32, -(-s // 64) * 64
     # the workspace: two query-term rows, the transposed log2e bias (fp32, one masked-logit row
     # per head, queries padded to 32 QT where the register dK/dV kernel runs), the dBias partials
+    # (with any window sums) and the dQ kernel's fp16 bias fragments
     r256 = lambda b: -(-b // 256) * 256
     qt = sqa // 32
     sqb = 32 * (4 if qt <= 4 else 8 if qt <= 8 else 12) if d == 32 and qt <= 12 else sqa
     biast = h * (ska + 1) * sqb * 4
-    partial = max(ws_bytes - 2 * r256(n * h * sqa * 4) - r256(biast), 0)
+    bfrag = h * sqa * ska * 2
+    partial = max(ws_bytes - 2 * r256(n * h * sqa * 4) - r256(biast) - r256(bfrag), 0)
     return {
         "attn_fwd": (4 * u, 3 * t + bias + km + t + row, 0),
-        "bwd_biast": (0.0, bias + biast, 0),
+        "bwd_biast": (0.0, bias + biast + bfrag, 0),
         # dQ = dS K is 2u; the kernel also recomputes S and dP (4u more)
-        "bwd_dq": (2 * u, 5 * t + row + bias + km + t, 2 * row),
+        "bwd_dq": (2 * u, 5 * t + row + bias + km + t, 2 * row + bfrag),
         "bwd_dkdv": (8 * u, 4 * t + row + bias + km + 2 * t, partial),
         "bwd_dbias": (0.0, dbias, partial),
     }

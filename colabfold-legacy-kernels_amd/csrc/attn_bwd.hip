@@ -48,6 +48,11 @@ struct BwdArgs {
     // head holds the masked logit (log2e kMaskedLogit), the bias a dead key's lane reads
     float* biast;
     float* partial;  // workspace [chunks][H][kblocks][SqA][64]
+    // workspace [H][SqA / 16][kblocks][2][64][8]: the dQ kernel's bias fragments. For each block
+    // of 16 queries and 64-key tile, part 0 holds for lane l = r + 16 g the bias of query r, keys
+    // 16 g .. +7, part 1 keys 16 g + 8 .. +15 (zero outside Sq and Sk), so that each of its bias
+    // loads is one contiguous 1 KB sweep
+    half_t* bfrag;
     // workspace [2][windows][N][H][Sk][D]: with more than one query window, each window's fp32
     // dK (unscaled) and dV sums over its queries, added up in window order by dkdv_sum_kernel
     float* dkv;
@@ -79,21 +84,6 @@ __device__ __forceinline__ half8 bld8(const half_t* p) { return *reinterpret_cas
 struct BH16 {
     half8 lo, hi;
 };
-
-__device__ __forceinline__ BH16 bload_h16(const half_t* p, int valid, bool vec) {
-    BH16 r;
-    if (vec && valid >= 16) {
-        r.lo = bld8(p);
-        r.hi = bld8(p + 8);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            r.lo[j] = j < valid ? p[j] : (half_t)0.f;
-            r.hi[j] = j + 8 < valid ? p[j + 8] : (half_t)0.f;
-        }
-    }
-    return r;
-}
 
 // ------------------------------------------------------------------------------------------
 // dQ (and delta): the forward's orientation, S^T = K Q^T and dP^T = V dO^T with a lane on one
@@ -211,24 +201,22 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 
     // bias of this lane's 16 keys k0 + 16 g .. +15, one key tile ahead of their use, in two
     // register sets that alternate by tile; when the tile comes up, a masked key or a key past
-    // Sk gets bias -inf, so its p, and with it its dS, is 0
-    const half_t* brow[T::kQB];
+    // Sk gets bias -inf, so its p, and with it its dS, is 0. The values come from the fragment
+    // copy the transposed-bias kernel writes: per 16-query block and key tile two 1 KB parts in
+    // lane order, read from a wave-uniform base (a block past SqA, whose queries are all past Sq,
+    // reads the last real block instead).
+    const int wq = __builtin_amdgcn_readfirstlane(q0w);
+    const half_t* bfr[T::kQB];
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) {
-        const int gq = q0w + 16 * qb + r16;
-        const int gqc = gq < a.Sq ? gq : a.Sq - 1;
-        brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
+        const int qblk = min((wq + 16 * qb) / 16, a.SqA / 16 - 1);
+        bfr[qb] = a.bfrag + ((int64_t)h * (a.SqA / 16) + qblk) * a.kblocks * 1024;
     }
     const auto fetch_bias = [&](int k0, BH16 (&b)[T::kQB]) {
-        if (a.bias_vec && k0 + T::kBK <= a.Sk) {
 #pragma unroll
-            for (int qb = 0; qb < T::kQB; ++qb) {
-                b[qb].lo = bld8(brow[qb] + k0);
-                b[qb].hi = bld8(brow[qb] + k0 + 8);
-            }
-        } else {
-#pragma unroll
-            for (int qb = 0; qb < T::kQB; ++qb) b[qb] = bload_h16(brow[qb] + k0, a.Sk - (k0 + 16 * g), a.bias_vec);
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            b[qb].lo = bld8(bfr[qb] + (k0 / T::kBK) * 1024 + 8 * lane);
+            b[qb].hi = bld8(bfr[qb] + (k0 / T::kBK) * 1024 + 512 + 8 * lane);
         }
     };
     const auto fix_bias = [&](int k0, BH16 (&b)[T::kQB], uint64_t keep64) {
@@ -1367,6 +1355,18 @@ __global__ __launch_bounds__(256) void attn_bwd_biast_kernel(BwdArgs a) {
                 q0 + tid < a.Sq ? kMaskedLogit2 : -INFINITY;
         }
     }
+    {
+        // the dQ kernel's fragments of this tile's two 16-query blocks: thread t writes block
+        // t / 128, part (t / 64) % 2, lane l = t % 64 (query l % 16, keys 16 (l / 16) + 8 part ..)
+        const int qb = tid >> 7, part = (tid >> 6) & 1, l = tid & 63;
+        const int qblk = q0 / 16 + qb;
+        if (qblk < a.SqA / 16) {
+            half8 f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = tile[16 * qb + (l & 15)][16 * (l >> 4) + 8 * part + j];
+            *reinterpret_cast<half8*>(a.bfrag + ((((int64_t)h * (a.SqA / 16) + qblk) * a.kblocks + kblk) * 2 + part) * 512 + 8 * l) = f;
+        }
+    }
 }
 
 // dbias[h][q][key] = the chunks' partials summed in chunk order. A workgroup takes 16 queries x
@@ -1446,7 +1446,7 @@ struct BwdPlan {
     int wtiles = 1, windows = 1;  // query windows of the dK/dV kernel
     size_t stage_lds = 0, dbias_lds = 0;
     int SqA = 0, SkA = 0, SqB = 0;
-    size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0, dkv_bytes = 0;
+    size_t delta_bytes = 0, biast_bytes = 0, partial_bytes = 0, dkv_bytes = 0, bfrag_bytes = 0;
     std::string error;
 };
 
@@ -1507,6 +1507,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
         p.SqB = 32 * p.QT;
         p.biast_bytes = round256((size_t)H * (p.SkA + 1) * p.SqB * sizeof(float));
         p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
+        p.bfrag_bytes = round256((size_t)H * p.SqA * p.SkA * sizeof(half_t));
         return p;
     }
     // row groups of the dK/dV kernel: at most the query tiles of a window, which they walk from
@@ -1564,11 +1565,12 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     p.biast_bytes = round256((size_t)H * (p.SkA + 1) * p.SqB * sizeof(float));
     p.partial_bytes = round256((size_t)p.chunks * H * p.kblocks * p.SqA * 64 * sizeof(float));
     p.dkv_bytes = p.windows > 1 ? round256((size_t)2 * p.windows * N * H * Sk * D * sizeof(float)) : 0;
+    p.bfrag_bytes = round256((size_t)H * p.SqA * p.SkA * sizeof(half_t));
     return p;
 }
 
 static size_t bwd_workspace_bytes(const BwdPlan& p) {
-    return 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes + p.dkv_bytes;
+    return 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes + p.dkv_bytes + p.bfrag_bytes;
 }
 
 template <int DP, int QG>
@@ -1784,6 +1786,7 @@ static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffe
     a.biast = reinterpret_cast<float*>(ws + 2 * p.delta_bytes);
     a.partial = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes);
     a.dkv = reinterpret_cast<float*>(ws + 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes);
+    a.bfrag = reinterpret_cast<half_t*>(ws + 2 * p.delta_bytes + p.biast_bytes + p.partial_bytes + p.dkv_bytes);
     a.N = (int)N; a.H = (int)H; a.Sq = (int)Sq; a.Sk = (int)Sk; a.D = (int)D;
     a.SqA = p.SqA;
     a.SqB = p.SqB;
