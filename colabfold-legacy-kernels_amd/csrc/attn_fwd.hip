@@ -88,6 +88,9 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     // two key tiles in flight: one being read by the MFMAs, the next being written
     __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kKsLd];
     __shared__ __attribute__((aligned(16))) half_t Vs2[2][T::kBK * T::kKsLd];
+    // where bias rows are whole 16-byte vectors: each wave's bias tiles (its 32 queries x 64 keys),
+    // two buffers, filled by direct-to-LDS loads (below)
+    __shared__ __attribute__((aligned(16))) half_t Bs[T::kWaves][2][4 * 520];
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -100,6 +103,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     const int q0 = qt * T::kBQ;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
 
     const int64_t qbase = n * a.qn + h * a.qh;
     const int64_t kbase = n * a.kn + h * a.kh;
@@ -202,9 +206,10 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         }
     };
 
-    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, one key tile ahead of their
-    // use, in two register sets that alternate by tile; when the tile comes up, a masked key's
-    // bias becomes the masked logit -1e4 and a key past Sk's -inf
+    // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, in a register set per tile
+    // parity: loaded one key tile ahead where rows are not whole 16-byte vectors, else read from
+    // LDS at the start of the tile (below); when the tile comes up, a masked key's bias becomes
+    // the masked logit -1e4 and a key past Sk's -inf
     const half_t* brow[T::kQB];
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) {
@@ -212,20 +217,41 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         const int gqc = gq < a.Sq ? gq : a.Sq - 1;
         brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
     }
-    // where bias rows are whole 16-byte vectors (and a head's bias spans under 2^31 bytes): buffer
-    // loads whose range is the head's bias block, from a fixed lane offset. Keys past Sk read the
-    // next row's values or zeros; they become -inf when their tile comes up.
+    // Where bias rows are whole 16-byte vectors (and a head's bias spans under 2^31 bytes) the
+    // bias goes through LDS: a lane's 16 keys of one query row are 32 bytes of a different row
+    // for each of 16 lanes, so register loads of them touch 16 cache lines per instruction, which
+    // measured a sixth of the kernel's time. Instead the wave loads its 32 x 64 bias tile with
+    // four direct-to-LDS loads (buffer_load ... lds) from a buffer whose range is the head's bias
+    // block, each a contiguous sweep of 8 rows x 128 bytes: lane 8 r + j of load m reads row 8 m + r,
+    // 16-byte segment (j - 2 (r / 2)) % 8, and lands at byte 1040 m + 16 (8 r + j) of the wave's
+    // buffer. The rotation and the 16-byte skew between loads put the 16 rows of each 16-lane read
+    // on distinct LDS banks. Rows past Sq read row Sq - 1 (their results are never stored); keys
+    // past Sk read the next row's values or zeros and become -inf when their tile comes up.
     const half_t* const bias_head = a.bias + (int64_t)h * a.Sq * a.Sk;
-    uint32_t boff[T::kQB];
+    uint32_t bdma[4];
 #pragma unroll
-    for (int qb = 0; qb < T::kQB; ++qb) boff[qb] = (uint32_t)((brow[qb] - bias_head) * 2);
-    const auto fetch_bias_vec = [&](int k0, H16 (&b)[T::kQB]) {
+    for (int m = 0; m < 4; ++m) {
+        const int r = lane >> 3, seg = ((lane & 7) - 2 * (r >> 1)) & 7;
+        const int gq = min(q0w + 8 * m + r, a.Sq - 1);
+        bdma[m] = (uint32_t)gq * (uint32_t)a.Sk * 2u + 16u * (uint32_t)seg;
+    }
+    const auto dma_bias = [&](int k0, int bb) {
         const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(bias_head + k0), 0,
                                                           (a.Sq * a.Sk - k0) * 2, 0x00020000);
 #pragma unroll
+        for (int m = 0; m < 4; ++m)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void*)&Bs[wv][bb][520 * m], 16, bdma[m], 0, 0, 0);
+    };
+    // this lane's 16 keys of query row 16 qb + r16 from the wave's buffer bb: segments 2 g and
+    // 2 g + 1, adjacent in LDS
+    const auto read_bias = [&](int bb, H16 (&b)[T::kQB]) {
+#pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
-            b[qb].lo = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[qb], 0, 0));
-            b[qb].hi = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rb, boff[qb] + 16, 0, 0));
+            const int m = 2 * qb + (r16 >> 3), r = r16 & 7;
+            const half_t* p = &Bs[wv][bb][520 * m + 8 * (8 * r + ((2 * g + 2 * (r >> 1)) & 7))];
+            b[qb].lo = ld8(p);
+            b[qb].hi = ld8(p + 8);
         }
     };
     const auto fetch_bias = [&](int k0, H16 (&b)[T::kQB]) {
@@ -263,9 +289,13 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         const half_t* Vs = Vs2[buf];
         bool more = true;
         if constexpr (decltype(vec)::value) {
+            // this tile's bias loads, issued a tile ago, are the only loads in flight: wait for
+            // them (the compiler does not order LDS reads after direct-to-LDS loads by itself)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            read_bias(buf, bias16);
             const int kn = min(k0 + T::kBK, k_last);
             fetch(kn);
-            fetch_bias_vec(kn, bias_next);
+            dma_bias(kn, buf ^ 1);
         } else {
             more = k0 + T::kBK < k_end;
             if (more) {
@@ -372,7 +402,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     const auto run = [&](auto vec) __attribute__((always_inline)) {
         fetch(0);
         if constexpr (decltype(vec)::value) {
-            fetch_bias_vec(0, biasA);
+            dma_bias(0, 0);
         } else {
             fetch_bias(0, biasA);
         }
@@ -383,6 +413,8 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             tile(vec, k0, 0, biasA, biasB);
             if (k0 + T::kBK < k_end) tile(vec, k0 + T::kBK, 1, biasB, biasA);
         }
+        // the last tile's bias loads (of itself, unused) land before the workgroup's LDS is freed
+        if constexpr (decltype(vec)::value) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
     if (k_end > 0) {
         if (a.bias_vec) {
