@@ -1045,7 +1045,12 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
 // workgroup's bias as fp16 (the original values, recovered exactly from the fp32 log2e form), so
 // s2 = log2e (scale S + bias) takes an fma with the fp16 operand read in place and a multiply.
 // The thirds' dK / dV sums meet in LDS once per row, thirds 1 and 2 into third 0 in that order.
-// Everything else is attn_bwd_dkdv_reg_kernel's.
+// The Q / dO tiles and the query terms of the next step go straight from memory into the idle
+// LDS buffer by direct-to-LDS loads (buffer_load ... lds), issued at the start of a step and
+// complete at its closing barrier: no staging registers and no LDS store instructions. The two
+// buffers (and the two term buffers) are separate arrays with compile-time selection, so the
+// compiler can tell that the step's LDS reads do not alias the loads in flight and does not wait
+// for them. Everything else is attn_bwd_dkdv_reg_kernel's.
 // ------------------------------------------------------------------------------------------
 template <bool DBIAS>
 __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
@@ -1056,9 +1061,12 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     constexpr int SqB = 32 * QT;
     constexpr int kBRow = SqB + 8;           // LDS bias row stride (halfs)
     __shared__ __attribute__((aligned(16))) half_t bias_l[65 * kBRow];  // rows: 64 keys, masked
-    __shared__ __attribute__((aligned(16))) half_t lds[2 * kBuf];
-    // query terms [buf][third][tile][-lse2 / c1 x 32, -delta x 32], then 768 zeros
-    __shared__ __attribute__((aligned(16))) float qterms[2 * 384 + 768];
+    __shared__ __attribute__((aligned(16))) half_t lds0[kBuf];
+    __shared__ __attribute__((aligned(16))) half_t lds1[kBuf];
+    // query terms of each buffer [third][tile][-lse2 / c1 x 32, -delta x 32] (384 of the first 512
+    // floats), then 384 zeros, the -delta a dead key's lane reads
+    __shared__ __attribute__((aligned(16))) float qterms0[512 + 384];
+    __shared__ __attribute__((aligned(16))) float qterms1[512 + 384];
     // thirds 1 and 2's dK / dV sums of a row: [third - 1][key group][float4 j][lane]
     __shared__ __attribute__((aligned(16))) float4 red[2 * 4 * 4 * 64];
 
@@ -1093,14 +1101,20 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
             }
         }
     }
-    if (tid < 192) reinterpret_cast<float4*>(qterms + 768)[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < 192) reinterpret_cast<float4*>(tid < 96 ? qterms0 + 512 : qterms1 + 128)[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // this wave's staging share of a step: tile (third sq3, tile si) of tensor (Q, dO)
     const int ti = wave >> 1, tensor = wave & 1, sq3 = ti >> 1, si = ti & 1;
-    const int crow = lane >> 2, ccol = (lane & 3) * 8;
-    const uint32_t cvoff = (uint32_t)((crow * DP + ccol) * 2);
-    const int cdst0 = (2 * sq3 + si) * kSub + tensor * kOs + 2 * reg_word(perm_row(crow, 8), ccol);
-    const int cdst1 = (2 * sq3 + si) * kSub + tensor * kOs + 2 * reg_word(perm_row(crow + 16, 8), ccol);
+    // as two direct-to-LDS loads of 16 LDS rows each: slot l of load i is LDS row R = 16 i + l / 4,
+    // position p = l % 4, which holds chunk p ^ ((R / 4) % 4) of tile row x (perm_row(x, 8) = R)
+    uint32_t dvoff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int R = 16 * i + (lane >> 2), p = lane & 3;
+        const int x = 8 * ((R >> 2) & 3) + 4 * (R >> 4) + (R & 3);
+        dvoff[i] = (uint32_t)((x * DP + 8 * (p ^ ((R >> 2) & 3))) * 2);
+    }
+    const int dst_off = (2 * sq3 + si) * kSub + tensor * kOs;
     const half_t* const csrc = tensor ? a.dout : a.q;
     // waves 0 and 1 stage the query terms: flat lane L < 96, tile L / 16 of [third][tile]
     const int qL = wave * kWave + lane;
@@ -1110,28 +1124,27 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     const auto row_nh = [&](int pass) -> int64_t {
         return (int64_t)(n_begin + (pass < rows ? pass : 0)) * a.H + h;
     };
-    half8 chk[2];
-    float4 qst;
-    const auto fetch_s = [&](int pass, int step) {
+    // step `step` of row `pass` into LDS buffer buf, by direct-to-LDS loads: this wave's tile, and
+    // (waves 0 and 1) the step's query terms, lane qL to float 4 qL of the buffer's terms (wave 1's
+    // lanes 32..63 write zeros into its unused tail)
+    const auto dma_s = [&](int pass, int step, int buf) {
         const int64_t nh = row_nh(pass);
         const int q0 = 32 * (sq3 * TT + 2 * step + si);
         const auto rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<half_t*>(csrc + (nh * a.Sq + q0) * DP), 0, max(a.Sq - q0, 0) * DP * 2, 0x00020000);
-        chk[0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff, 0, 0));
-        chk[1] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rs, cvoff + 16u * DP * 2u, 0, 0));
+        half_t* dst = (buf ? lds1 : lds0) + dst_off;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16, dvoff[i], 0, 0, 0);
         if (wave < 2) {
             const int tg = (qt_t >> 1) * TT + 2 * step + (qt_t & 1);
             const auto rq = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(a.qstat + nh * a.SqA * 2), 0, a.SqA * 2 * 4, 0x00020000);
-            qst = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                rq, qL < 96 ? ((uint32_t)(64 * tg) + qt_f) * 4u : 0x80000000u, 0, 0));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rq, (__attribute__((address_space(3))) void*)((buf ? qterms1 : qterms0) + 256 * wave), 16,
+                qL < 96 ? ((uint32_t)(64 * tg) + qt_f) * 4u : 0x80000000u, 0, 0, 0);
         }
-    };
-    const auto stage = [&](int buf) {
-        half_t* dst = lds + buf * kBuf;
-        *reinterpret_cast<half8*>(dst + cdst0) = chk[0];
-        *reinterpret_cast<half8*>(dst + cdst1) = chk[1];
-        if (wave < 2 && qL < 96) *reinterpret_cast<float4*>(qterms + buf * 384 + 4 * qL) = qst;
     };
 
     half8 kopn, vopn;
@@ -1155,9 +1168,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
 
     if (rows > 0) {
         fetch_kv(0);
-        fetch_s(0, 0);
-        stage(0);
-        fetch_s(0, 1);
+        dma_s(0, 0, 0);
     }
     __syncthreads();
 
@@ -1168,8 +1179,8 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
         const half8 vop = alive ? vopn : bzero8();
         // a dead key's lane: the masked-logit bias row, and -delta from the zeroed area
         const half_t* const brow = bias_l + (alive ? klocal : 64) * kBRow + q3 * TT * 32 + 8 * g;
-        const float* const qtS = qterms + q3 * 128 + 8 * g;
-        const float* const qtD = qtS + 32 + (alive ? 0 : 768);
+        const int qtS = q3 * 128 + 8 * g;
+        const int qtD = qtS + 32 + (alive ? 0 : 512);
         float4v accv[2], acck[2];
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
@@ -1181,9 +1192,10 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
 #pragma unroll
         for (int st = 0; st < kSteps; ++st) {
             const int par = st & 1;  // kSteps is even
-            stage(par ^ 1);
-            fetch_s(pass + (st + 2) / kSteps, (st + 2) % kSteps);
-            const half_t* buf = lds + par * kBuf + q3 * 2 * kSub;
+            // the next step's tiles into the other buffer, whose last reads ended at the barrier
+            dma_s(pass + (st + 1) / kSteps, (st + 1) % kSteps, par ^ 1);
+            const half_t* buf = (par ? lds1 : lds0) + q3 * 2 * kSub;
+            const float* qtb = par ? qterms1 : qterms0;
             float x[2][8];
             float4v dp[2][2];
 #pragma unroll
@@ -1191,12 +1203,12 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
                 const int u = 2 * st + i;
                 const half_t* Qs = buf + i * kSub;
                 const half_t* Os = Qs + kOs;
-                const int qo = par * 384 + 64 * i;
+                const int qo = 64 * i;
                 const half8 bb = *reinterpret_cast<const half8*>(brow + 32 * u);
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb) {
-                    float4v sacc = *reinterpret_cast<const float4v*>(qtS + qo + 4 * qb);
-                    dp[i][qb] = *reinterpret_cast<const float4v*>(qtD + qo + 4 * qb);
+                    float4v sacc = *reinterpret_cast<const float4v*>(qtb + qtS + qo + 4 * qb);
+                    dp[i][qb] = *reinterpret_cast<const float4v*>(qtb + qtD + qo + 4 * qb);
                     const int w = 2 * reg_word(16 * qb + r16, 8 * g);
                     const half8 qa = *reinterpret_cast<const half8*>(Qs + w);
                     const half8 oa = *reinterpret_cast<const half8*>(Os + w);
