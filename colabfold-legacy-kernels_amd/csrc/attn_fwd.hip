@@ -86,8 +86,11 @@ template <int DP, bool LSE, bool GATE, bool TRIM>
 __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_fwd_kernel(FwdArgs a) {
     using T = FwdTile<DP>;
     // two key tiles in flight: one being read by the MFMAs, the next being written
-    __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kKsLd];
-    __shared__ __attribute__((aligned(16))) half_t Vs2[2][T::kBK * T::kKsLd];
+    // (at DP = 32 four unpadded arrays instead, one per tensor and buffer: below)
+    __shared__ __attribute__((aligned(16))) half_t Ks2[DP == 32 ? 1 : 2][T::kBK * T::kKsLd];
+    __shared__ __attribute__((aligned(16))) half_t Vs2[DP == 32 ? 1 : 2][T::kBK * T::kKsLd];
+    constexpr int kD32 = DP == 32 ? T::kBK * 32 : 8;
+    __shared__ __attribute__((aligned(16))) half_t K32a[kD32], K32b[kD32], V32a[kD32], V32b[kD32];
     // where bias rows are whole 16-byte vectors: each wave's bias tiles (its 32 queries x 64 keys),
     // two buffers, filled by direct-to-LDS loads (below)
     __shared__ __attribute__((aligned(16))) half_t Bs[T::kWaves][2][4 * 520];
@@ -197,12 +200,58 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
     const auto stage = [&](int buf, uint64_t keep) {
-        half_t* Ks = Ks2[buf];
-        half_t* Vs = Vs2[buf];
+        if constexpr (DP == 32) {
+            // the tile came by direct-to-LDS loads (below): once they have landed, each wave
+            // zeroes the K rows of the masked keys in its own fragment block
+            if (keep != ~0ull) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                const int key = 16 * ((lane & 15) >> 2) + 4 * wv + (lane & 3);
+                if (!((keep >> key) & 1u))
+                    *reinterpret_cast<half8*>((buf ? K32b : K32a) + 512 * wv + 8 * lane) = zero8();
+            }
+        } else {
+            half_t* Ks = Ks2[buf];
+            half_t* Vs = Vs2[buf];
 #pragma unroll
-        for (int i = 0; i < T::kCPT; ++i) {
-            *reinterpret_cast<half8*>(&Ks[kdst[i]]) = (keep >> krow[i]) & 1u ? kreg[i] : zero8();
-            *reinterpret_cast<half8*>(&Vs[vdst[i]]) = vreg[i];
+            for (int i = 0; i < T::kCPT; ++i) {
+                *reinterpret_cast<half8*>(&Ks[kdst[i]]) = (keep >> krow[i]) & 1u ? kreg[i] : zero8();
+                *reinterpret_cast<half8*>(&Vs[vdst[i]]) = vreg[i];
+            }
+        }
+    };
+    // At DP = 32 the K and V tiles go from memory straight into LDS by direct-to-LDS loads
+    // (buffer_load ... lds), one 1 KB load of each per wave, issued with the next tile's other
+    // loads and complete at the tile's closing barrier: no staging registers and no LDS stores.
+    // Wave w loads K's fragment block w (slot l: key 16 (l % 16 / 4) + 4 w + l % 4, d 8 (l / 16)
+    // .. +7, the layout above) and V rows 16 w .. +15 unpadded (slot l: row 16 w + l / 4, d
+    // 8 (l % 4) ..). Masked keys' K rows are zeroed in LDS after the loads land (stage).
+    uint32_t kdma = 0u, vdma = 0u;
+    if constexpr (DP == 32) {
+        const int kr = 16 * ((lane & 15) >> 2) + 4 * wave + (lane & 3), kc = 8 * (lane >> 4);
+        const int vr = 16 * wave + (lane >> 2), vc = 8 * (lane & 3);
+        kdma = kc < a.D ? (uint32_t)((kr * a.ks + kc) * 2) : 0x80000000u;
+        vdma = vc < a.D ? (uint32_t)((vr * a.ks + vc) * 2) : 0x80000000u;
+    }
+    const auto dma_kv = [&](int k0, int buf) {
+        const int rows = min(a.Sk - k0, T::kBK);
+        const int64_t kofs = (int64_t)k0 * a.ks * 2;
+        // (a wave-uniform range, kept in a scalar register: the loads need scalar descriptors)
+        const int range = __builtin_amdgcn_readfirstlane(rows * (int)a.ks * 2);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb_base + kofs), 0, range, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb_base + kofs), 0, range, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (__attribute__((address_space(3))) void*)((buf ? K32b : K32a) + 512 * wv), 16, kdma, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (__attribute__((address_space(3))) void*)((buf ? V32b : V32a) + 512 * wv), 16, vdma, 0, 0, 0);
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
+        mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
+    };
+    // the next tile's K, V and mask byte into buffer buf
+    const auto fetch_kv = [&](int k0, int buf) {
+        if constexpr (DP == 32) {
+            dma_kv(k0, buf);
+        } else {
+            fetch(k0);
         }
     };
 
@@ -285,8 +334,8 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     const int k_last = (k_end - 1) / T::kBK * T::kBK;
     const auto tile = [&](auto vec, int k0, int buf, H16 (&bias16)[T::kQB],
                           H16 (&bias_next)[T::kQB]) __attribute__((always_inline)) {
-        const half_t* Ks = Ks2[buf];
-        const half_t* Vs = Vs2[buf];
+        const half_t* Ks = DP == 32 ? (buf ? K32b : K32a) : Ks2[buf & (DP == 32 ? 0 : 1)];
+        const half_t* Vs = DP == 32 ? (buf ? V32b : V32a) : Vs2[buf & (DP == 32 ? 0 : 1)];
         bool more = true;
         if constexpr (decltype(vec)::value) {
             // this tile's bias loads, issued a tile ago, are the only loads in flight: wait for
@@ -294,12 +343,12 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             read_bias(buf, bias16);
             const int kn = min(k0 + T::kBK, k_last);
-            fetch(kn);
+            fetch_kv(kn, buf ^ 1);
             dma_bias(kn, buf ^ 1);
         } else {
             more = k0 + T::kBK < k_end;
             if (more) {
-                fetch(k0 + T::kBK);
+                fetch_kv(k0 + T::kBK, buf ^ 1);
                 fetch_bias(k0 + T::kBK, bias_next);
             }
         }
@@ -321,8 +370,8 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             }
         }
 
-        // natural-domain logits t = scale s + bias: a masked key's s is 0 and its bias the masked
-        // logit, a key past Sk has bias -inf
+        // natural-domain logits t = scale s + bias: a masked key's s is 0 (its K row staged as
+        // zeros) and its bias the masked logit, a key past Sk has bias -inf
         float m_tile[T::kQB];
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
@@ -380,7 +429,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         // O^T += V^T P^T: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4; slot 8 g + j of
         // contraction step kt is key 16 g + 8 kt + j, which is where P^T already sits. V^T is
         // read transposed from the row-major V tile.
-        const auto vrow = [&](int r) { return Vs + r * T::kKsLd; };
+        const auto vrow = [&](int r) { return Vs + r * (DP == 32 ? 32 : T::kKsLd); };
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -400,7 +449,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
 
     H16 biasA[T::kQB], biasB[T::kQB];
     const auto run = [&](auto vec) __attribute__((always_inline)) {
-        fetch(0);
+        fetch_kv(0, 0);
         if constexpr (decltype(vec)::value) {
             dma_bias(0, 0);
         } else {
