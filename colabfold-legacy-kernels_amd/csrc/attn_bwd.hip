@@ -104,8 +104,11 @@ template <int DP>
 __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_bwd_dq_kernel(BwdArgs a) {
     using T = DqTile<DP>;
     // two key tiles in flight: one being read by the MFMAs, the next being written
-    __shared__ __attribute__((aligned(16))) half_t Ks2[2][T::kBK * T::kLd];
-    __shared__ __attribute__((aligned(16))) half_t Vs2[2][T::kBK * T::kLd];
+    // (at DP = 32 four unpadded arrays instead, one per tensor and buffer: below)
+    __shared__ __attribute__((aligned(16))) half_t Ks2[DP == 32 ? 1 : 2][T::kBK * T::kLd];
+    __shared__ __attribute__((aligned(16))) half_t Vs2[DP == 32 ? 1 : 2][T::kBK * T::kLd];
+    constexpr int kD32 = DP == 32 ? T::kBK * 32 : 8;
+    __shared__ __attribute__((aligned(16))) half_t K32a[kD32], K32b[kD32], V32a[kD32], V32b[kD32];
 
     const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
@@ -115,6 +118,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
     const int n = rest % a.N, h = rest / a.N;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     const int64_t nh = (int64_t)n * a.H + h;
     const int64_t qbase = nh * a.Sq * a.D, kbase = nh * a.Sk * a.D;
     const int q0w = qt * T::kBQ + wave * (T::kQB * 16);
@@ -189,11 +193,63 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
         const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
         mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
+    // At DP = 32 the K and V tiles go from memory straight into LDS by direct-to-LDS loads
+    // (buffer_load ... lds), one 1 KB load of each per wave, issued at the start of the previous
+    // tile and complete at its closing barrier. Their rows are unpadded 64 bytes with the 16-byte
+    // chunks of LDS row R at chunk position c ^ ((R / 4) % 4), so the row-form reads of 16
+    // consecutive rows fall on 16 distinct bank groups: slot l of wave w's load is LDS row
+    // R = 16 w + l / 4 (key x with perm_row(x, 16) = R), position l % 4. Masked keys' K rows are
+    // zeroed in LDS once the loads have landed.
+    uint32_t kvdma = 0u;
+    int dkey = 0;
+    if constexpr (DP == 32) {
+        const int R = 16 * wave + (lane >> 2), pos = lane & 3;
+        dkey = 16 * ((R >> 2) & 3) + 4 * (R >> 4) + (R & 3);
+        const int col = 8 * (pos ^ ((R >> 2) & 3));
+        kvdma = col < a.D ? (uint32_t)((dkey * a.D + col) * 2) : 0x80000000u;
+    }
+    const auto dma_kv = [&](int k0, int buf) {
+        const int rows = min(a.Sk - k0, T::kBK);
+        const int64_t kofs = (int64_t)k0 * a.D * 2;
+        const int range = __builtin_amdgcn_readfirstlane(rows * a.D * 2);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb_base + kofs), 0, range, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb_base + kofs), 0, range, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (__attribute__((address_space(3))) void*)((buf ? K32b : K32a) + 512 * wv), 16, kvdma, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (__attribute__((address_space(3))) void*)((buf ? V32b : V32a) + 512 * wv), 16, kvdma, 0, 0, 0);
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
+        mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
+    };
+    const auto fetch_kv = [&](int k0, int buf) {
+        if constexpr (DP == 32) {
+            dma_kv(k0, buf);
+        } else {
+            fetch(k0);
+        }
+    };
     const auto stage = [&](int buf, uint64_t keep) {
+        if constexpr (DP == 32) {
+            if (keep != ~0ull) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                if (!((keep >> dkey) & 1u))
+                    *reinterpret_cast<half8*>((buf ? K32b : K32a) + 512 * wv + 8 * lane) = bzero8();
+            }
+        } else {
 #pragma unroll
-        for (int i = 0; i < T::kCPT; ++i) {
-            *reinterpret_cast<half8*>(&Ks2[buf][kdst[i]]) = (keep >> krow[i]) & 1u ? kreg[i] : bzero8();
-            *reinterpret_cast<half8*>(&Vs2[buf][kdst[i]]) = vreg[i];
+            for (int i = 0; i < T::kCPT; ++i) {
+                *reinterpret_cast<half8*>(&Ks2[buf][kdst[i]]) = (keep >> krow[i]) & 1u ? kreg[i] : bzero8();
+                *reinterpret_cast<half8*>(&Vs2[buf][kdst[i]]) = vreg[i];
+            }
+        }
+    };
+    // LDS address of tile row r (after the row permutation), chunk 8 c: padded rows, or at DP = 32
+    // the swizzled unpadded rows
+    const auto kv_at = [&](const half_t* t, int R, int c) -> const half_t* {
+        if constexpr (DP == 32) {
+            return t + 32 * R + 8 * (c ^ ((R >> 2) & 3));
+        } else {
+            return t + R * T::kLd + 8 * c;
         }
     };
 
@@ -237,11 +293,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 
     uint64_t keep_cur = 0u;
     const auto tile = [&](int k0, int buf, BH16 (&bias16)[T::kQB], BH16 (&bias_next)[T::kQB]) {
-        const half_t* Ks = Ks2[buf];
-        const half_t* Vs = Vs2[buf];
+        const half_t* Ks = DP == 32 ? (buf ? K32b : K32a) : Ks2[buf & (DP == 32 ? 0 : 1)];
+        const half_t* Vs = DP == 32 ? (buf ? V32b : V32a) : Vs2[buf & (DP == 32 ? 0 : 1)];
         const bool more = k0 + T::kBK < a.Sk;
         if (more) {
-            fetch(k0 + T::kBK);
+            fetch_kv(k0 + T::kBK, buf ^ 1);
             fetch_bias(k0 + T::kBK, bias_next);
         }
         // every key of the tile kept and inside Sk: the bias stands as loaded
@@ -263,8 +319,8 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
                 }
 #pragma unroll
                 for (int ks = 0; ks < T::kKS; ++ks) {
-                    const half8 kop = bld8(&Ks[krw * T::kLd + 32 * ks + 8 * g]);
-                    const half8 vop = bld8(&Vs[krw * T::kLd + 32 * ks + 8 * g]);
+                    const half8 kop = bld8(kv_at(Ks, krw, 4 * ks + g));
+                    const half8 vop = bld8(kv_at(Vs, krw, 4 * ks + g));
 #pragma unroll
                     for (int qb = 0; qb < T::kQB; ++qb) {
                         s[k2][qb] = mfma16x16x32(kop, qop[qb][ks], s[k2][qb]);
@@ -294,8 +350,17 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 #pragma unroll
             for (int db = 0; db < T::kDB; ++db) {
                 // K^T read transposed from the row-major K tile: slots are keys 16 g + 8 kt + j
-                const half8 kto = lds_operand_tr([&](int r) { return Ks + perm_row(r, 16) * T::kLd; },
-                                                 2 * g + kt, r16, 4 * db, DP / 4);
+                half8 kto;
+                if constexpr (DP == 32) {
+                    const int j = r16 >> 2, c = r16 & 3;
+                    const int Rl = perm_row(16 * g + 8 * kt + j, 16), Rh = perm_row(16 * g + 8 * kt + 4 + j, 16);
+                    const half4 lo = lds_read_tr16(Ks + 32 * Rl + 8 * (c ^ ((Rl >> 2) & 3)) + 4 * db);
+                    const half4 hi = lds_read_tr16(Ks + 32 * Rh + 8 * (c ^ ((Rh >> 2) & 3)) + 4 * db);
+                    kto = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                } else {
+                    kto = lds_operand_tr([&](int r) { return Ks + perm_row(r, 16) * T::kLd; },
+                                         2 * g + kt, r16, 4 * db, DP / 4);
+                }
 #pragma unroll
                 for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[qb], acc[db][qb]);
             }
@@ -310,7 +375,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 
     BH16 biasA[T::kQB], biasB[T::kQB];
     if (a.Sk > 0) {
-        fetch(0);
+        fetch_kv(0, 0);
         fetch_bias(0, biasA);
         keep_cur = __ballot(mbyte != 0u);
         stage(0, keep_cur);
