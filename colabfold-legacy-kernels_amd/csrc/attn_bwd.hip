@@ -70,6 +70,8 @@ struct BwdArgs {
     int kscale;  // 0 where c1 stands in for a negligible scale: the dK/dV kernel's K is then zero
     int bias_vec;
     int dbias_vec;  // dbias rows are whole 16-byte vectors (Sk % 4 == 0, 16-byte aligned)
+    // division by the dQ kernel's query tiles per (n, h), by N, kblocks, chunks and windows
+    FastDiv fqt, fn, fkb, fch, fwin;
 };
 
 __device__ __forceinline__ half8 bzero8() {
@@ -110,12 +112,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
     constexpr int kD32 = DP == 32 ? T::kBK * 32 : 8;
     __shared__ __attribute__((aligned(16))) half_t K32a[kD32], K32b[kD32], V32a[kD32], V32b[kD32];
 
-    const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
     // head-major order: an XCD's contiguous run of items covers few heads, so the bias rows
     // it reads stay in its L2
-    const int qt = item % QT, rest = item / QT;
-    const int n = rest % a.N, h = rest / a.N;
+    const int rest = fdiv(item, a.fqt), qt = item - rest * (int)a.fqt.d;
+    const int h = fdiv(rest, a.fn), n = rest - h * a.N;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(wave);
@@ -479,9 +480,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
     const int item = xcd_item(blockIdx.x, gridDim.x);
     // head-major order, as in the forward: an XCD's run of items reads few heads' bias columns;
     // the key blocks of one query window and chunk are neighbours, so they share Q and dO in L2
-    const int kblk = item % a.kblocks, rest = item / a.kblocks;
-    const int win = rest % a.windows, rest2 = rest / a.windows;
-    const int c = rest2 % a.chunks, h = rest2 / a.chunks;
+    const int rest = fdiv(item, a.fkb), kblk = item - rest * a.kblocks;
+    const int rest2 = fdiv(rest, a.fwin), win = rest - rest2 * a.windows;
+    const int h = fdiv(rest2, a.fch), c = rest2 - h * a.chunks;
     const int n_begin = c * a.chunk;
     const int n_end = min(a.N, n_begin + a.chunk);
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -620,7 +621,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
         const int n = n_begin + rg + QG * pass;
         const int64_t nh = (int64_t)(n < n_end ? n : n_begin) * a.H + h;
         const int kc = kin ? key : 0;
-        mbn = (uint32_t)a.kmask[(nh / a.H) * a.Sk + kc];
+        mbn = (uint32_t)a.kmask[(int64_t)(n < n_end ? n : n_begin) * a.Sk + kc];
 #pragma unroll
         for (int ks = 0; ks < T::kKS; ++ks) {
             const int d0 = 32 * ks + 8 * g;
@@ -885,8 +886,8 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
     // head-major order: an XCD's run of items reads few heads' bias columns
-    const int kblk = item % a.kblocks, rest = item / a.kblocks;
-    const int c = rest % a.chunks, h = rest / a.chunks;
+    const int rest = fdiv(item, a.fkb), kblk = item - rest * a.kblocks;
+    const int h = fdiv(rest, a.fch), c = rest - h * a.chunks;
     const int n_begin = c * a.chunk;
     const int rows = min(a.N, n_begin + a.chunk) - n_begin;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -923,9 +924,8 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
     const uint32_t qt_f = (uint32_t)(4 * (lane & 15));
 
     // row `pass` of the chunk, clamped to a real row past the end (its data is staged, never read)
-    const auto row_nh = [&](int pass) -> int64_t {
-        return (int64_t)(n_begin + (pass < rows ? pass : 0)) * a.H + h;
-    };
+    const auto row_n = [&](int pass) -> int { return n_begin + (pass < rows ? pass : 0); };
+    const auto row_nh = [&](int pass) -> int64_t { return (int64_t)row_n(pass) * a.H + h; };
     half8 chk[2];
     float4 qst;
     const auto fetch_s = [&](int pass, int step) {
@@ -956,7 +956,7 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
     const auto fetch_kv = [&](int pass) {
         const int64_t nh = row_nh(pass);
         const int kc = kin ? key : 0;
-        mbn = (uint32_t)a.kmask[(nh / a.H) * a.Sk + kc];
+        mbn = (uint32_t)a.kmask[(int64_t)row_n(pass) * a.Sk + kc];
         const int64_t off = (nh * a.Sk + kc) * DP + 8 * g;
         kopn = bld8(a.k + off);
         vopn = bld8(a.v + off);
@@ -1136,8 +1136,8 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     __shared__ __attribute__((aligned(16))) float4 red[2 * 4 * 4 * 64];
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
-    const int kblk = item % a.kblocks, rest = item / a.kblocks;
-    const int c = rest % a.chunks, h = rest / a.chunks;
+    const int rest = fdiv(item, a.fkb), kblk = item - rest * a.kblocks;
+    const int h = fdiv(rest, a.fch), c = rest - h * a.chunks;
     const int n_begin = c * a.chunk;
     const int rows = min(a.N, n_begin + a.chunk) - n_begin;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -1186,9 +1186,8 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     const int qt_t = qL >> 4;
     const uint32_t qt_f = (uint32_t)(4 * (qL & 15));
 
-    const auto row_nh = [&](int pass) -> int64_t {
-        return (int64_t)(n_begin + (pass < rows ? pass : 0)) * a.H + h;
-    };
+    const auto row_n = [&](int pass) -> int { return n_begin + (pass < rows ? pass : 0); };
+    const auto row_nh = [&](int pass) -> int64_t { return (int64_t)row_n(pass) * a.H + h; };
     // step `step` of row `pass` into LDS buffer buf, by direct-to-LDS loads: this wave's tile, and
     // (waves 0 and 1) the step's query terms, lane qL to float 4 qL of the buffer's terms (wave 1's
     // lanes 32..63 write zeros into its unused tail)
@@ -1217,7 +1216,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     const auto fetch_kv = [&](int pass) {
         const int64_t nh = row_nh(pass);
         const int kc = kin ? key : 0;
-        mbn = (uint32_t)a.kmask[(nh / a.H) * a.Sk + kc];
+        mbn = (uint32_t)a.kmask[(int64_t)row_n(pass) * a.Sk + kc];
         const int64_t off = (nh * a.Sk + kc) * DP + 8 * g;
         kopn = bld8(a.k + off);
         vopn = bld8(a.v + off);
@@ -1871,6 +1870,11 @@ static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffe
     a.kblocks = p.kblocks;
     a.chunk = p.chunk;
     a.chunks = p.chunks;
+    a.fqt = fast_div((Sq + DqTile<32>::kBQ - 1) / DqTile<32>::kBQ);  // kBQ is the same at every DP
+    a.fn = fast_div(N);
+    a.fkb = fast_div(p.kblocks);
+    a.fch = fast_div(p.chunks);
+    a.fwin = fast_div(p.windows);
     a.wtiles = p.wtiles;
     a.windows = p.windows;
     a.scale = scale;

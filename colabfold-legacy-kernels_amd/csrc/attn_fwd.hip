@@ -36,6 +36,7 @@ struct FwdArgs {
     float scale;
     int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0), one head's bias < 2^31 bytes
     int head_major;  // work items head-major ([N,H,S,D] tensors), else row-major (packed rows)
+    FastDiv fqt, fn, fh;  // division by the query tiles per (n, h), by N and by H (set at launch)
 };
 
 template <int DP>
@@ -95,14 +96,14 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     // two buffers, filled by direct-to-LDS loads (below)
     __shared__ __attribute__((aligned(16))) half_t Bs[T::kWaves][2][4 * 520];
 
-    const int QT = (a.Sq + T::kBQ - 1) / T::kBQ;
     const int item = xcd_item(blockIdx.x, gridDim.x);
     // head-major order for [N,H,S,D] tensors: an XCD's contiguous run of items covers few
     // heads, so the bias rows it reads stay in its L2; packed rows hold every head of a row n
     // together, so there the heads of one row run together instead
-    const int qt = item % QT, rest = item / QT;
-    const int n = a.head_major ? rest % a.N : rest / a.H;
-    const int h = a.head_major ? rest / a.N : rest % a.H;
+    const int rest = fdiv(item, a.fqt), qt = item - rest * (int)a.fqt.d;
+    const int nh_major = fdiv(rest, a.fn), nh_minor = fdiv(rest, a.fh);
+    const int n = a.head_major ? rest - nh_major * a.N : nh_minor;
+    const int h = a.head_major ? nh_major : rest - nh_minor * a.H;
     const int q0 = qt * T::kBQ;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
@@ -521,9 +522,13 @@ static int launch_fwd(hipStream_t stream, int device, const FwdArgs& a) {
     const int64_t grid = qt * a.H * a.N;
     if (grid == 0) return ok();
     if (grid > INT32_MAX) return invalid("attention: too many work items");
+    FwdArgs b = a;
+    b.fqt = fast_div(qt);
+    b.fn = fast_div(a.N);
+    b.fh = fast_div(a.H);
     stage_mark(stream, 0);
     hipLaunchKernelGGL((attn_fwd_kernel<DP, LSE, GATE, TRIM>), dim3((unsigned)grid),
-                       dim3(T::kThreads), 0, stream, a);
+                       dim3(T::kThreads), 0, stream, b);
     stage_mark(stream, 1);
     return launch_status("attention");
 }

@@ -141,6 +141,27 @@ __device__ __forceinline__ float wave_xor_max4(float v) {
 // Work item of a 1-D launch, with consecutive items on the same XCD: the dispatcher deals
 // workgroups round-robin over the 8 XCDs, so item i of XCD x is slot x's i-th workgroup.
 // Neighbouring items share K/V (or weights) through that XCD's L2.
+// Division of n < 2^31 by a runtime divisor 1 <= d < 2^31 as a multiply-high and a shift, so a
+// work item's decomposition runs on the scalar unit instead of a VALU division sequence
+// (Granlund and Montgomery's round-up method: mul = ceil(2^p / d), p = 31 + ceil(log2 d), exact
+// for every n < 2^31; d = 1 has mul = 0).
+struct FastDiv {
+    uint32_t mul = 0, shift = 0, d = 1;
+};
+inline FastDiv fast_div(int64_t d) {
+    FastDiv f;
+    f.d = (uint32_t)(d < 1 ? 1 : d);
+    if (f.d == 1) return f;
+    uint32_t l = 0;
+    while ((1ull << l) < f.d) ++l;
+    f.mul = (uint32_t)(((1ull << (31 + l)) + f.d - 1) / f.d);
+    f.shift = l - 1;
+    return f;
+}
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+    return f.mul ? (int)(__umulhi((uint32_t)n, f.mul) >> f.shift) : n;
+}
+
 __device__ __forceinline__ int xcd_item(int linear, int count) {
     constexpr int kXcds = 8;
     const int x = linear % kXcds, s = linear / kXcds;
