@@ -122,6 +122,32 @@ def test_tiny_shapes(hip, sq, sk, d):
     check(got, ref, "sq=%d sk=%d d=%d" % (sq, sk, d))
 
 
+@pytest.mark.parametrize("sq,sk,d", [(96, 96, 32), (384, 384, 32), (70, 83, 16), (130, 130, 64)])
+def test_masked_key_rows_do_not_matter(hip, sq, sk, d):
+    """A masked key's logit is the masked logit whatever its K row (volta_attn.h:9-14), and its
+    dS is 0: K rows of masked keys filled with large values (+-3e4) give out, lse, dq, dv and
+    dbias bit-identical to zero rows, and dK identical. The forward and dQ kernels load K tiles
+    straight into LDS at D <= 32 and zero the masked rows there; a missed row would put
+    q.k scale + bias in place of the masked logit."""
+    n, h = 2, 3
+    q, k, v, bias, km, dout = inputs(n, h, sq, sk, d, seed=11, masked_rows=0.3)
+    assert (km == 0).any() and (km != 0).any()
+    rng = np.random.default_rng(12)
+    dead = (km == 0)[:, None, :, None]
+    k_zero = np.where(dead, np.float16(0), k).astype(np.float16)
+    big = (np.sign(rng.standard_normal(k.shape)) * 3e4).astype(np.float16)
+    k_big = np.where(dead, big, k).astype(np.float16)
+    scale = float(d) ** -0.5
+    res = []
+    for kk in (k_zero, k_big):
+        tq, tk, tv, tb, tm, tdo = dev(q, kk, v, bias, km, dout)
+        out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale, 64, 64 if d == 64 else 32)
+        res.append(host(out, lse, *hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale)))
+    for name, x, y in zip(("out", "lse", "dq", "dk", "dv", "dbias"), *res):
+        assert np.isfinite(y).all(), name + " not finite with large masked K rows"
+        assert np.array_equal(x, y), name + " depends on the K rows of masked keys"
+
+
 @pytest.mark.parametrize("n", [63, 64, 96])
 def test_batch_sizes(hip, n):
     got, ref = run(hip, n=n, h=2, sq=64, sk=64, d=32)
