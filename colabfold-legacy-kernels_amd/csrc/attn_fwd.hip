@@ -317,13 +317,23 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         }
     };
     const auto fix_bias = [&](int k0, H16 (&b)[T::kQB], uint64_t keep64) {
-        const int kvalid = a.Sk - (k0 + 16 * g);
-        const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
-        const uint32_t keep = (uint32_t)(keep64 >> (16 * g)) & inside;
-        if (keep != 0xffffu) {
+        if (k0 + T::kBK <= a.Sk) {
+            // every key of the tile inside Sk (a uniform test): only the masked logit fills in
+            const uint32_t keep = (uint32_t)(keep64 >> (16 * g)) & 0xffffu;
+            if (keep != 0xffffu) {
 #pragma unroll
-            for (int qb = 0; qb < T::kQB; ++qb)
-                fill_bias16(b[qb].lo, b[qb].hi, keep, inside, (half_t)kMaskedLogit, (half_t)(-INFINITY));
+                for (int qb = 0; qb < T::kQB; ++qb)
+                    fill_bias16(b[qb].lo, b[qb].hi, keep, 0xffffu, (half_t)kMaskedLogit, (half_t)kMaskedLogit);
+            }
+        } else {
+            const int kvalid = a.Sk - (k0 + 16 * g);
+            const uint32_t inside = kvalid >= 16 ? 0xffffu : kvalid <= 0 ? 0u : (1u << kvalid) - 1u;
+            const uint32_t keep = (uint32_t)(keep64 >> (16 * g)) & inside;
+            if (keep != 0xffffu) {
+#pragma unroll
+                for (int qb = 0; qb < T::kQB; ++qb)
+                    fill_bias16(b[qb].lo, b[qb].hi, keep, inside, (half_t)kMaskedLogit, (half_t)(-INFINITY));
+            }
         }
     };
 
