@@ -126,9 +126,18 @@ def _stream(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+_ONES = {}
+
+
 def _one(like, dtype):
-    """The one-element buffer the FFI takes for an absent optional input or result."""
-    return torch.zeros(1, dtype=dtype, device=like.device)
+    """The one-element buffer the FFI takes for an absent optional input, or for a result that is
+    not produced (never written, never returned). One zero buffer per device and dtype is kept for
+    the process, so a call adds no allocation or fill of its own."""
+    key = (like.device, dtype)
+    t = _ONES.get(key)
+    if t is None:
+        t = _ONES[key] = torch.zeros(1, dtype=dtype, device=like.device)
+    return t
 
 
 def attention_fwd(q, k, v, bias, kmask, scale, block_q=64, block_k=32, want_lse=True, out=None,
@@ -301,7 +310,7 @@ def opm_update(lhs, t, bias, norm, residual=None, eps=1e-3, out=None):
     lhs [B,K], t [K,D,F] fp16, bias [F], norm [B,D] fp32. residual may be `out` itself."""
     b, (d, f) = lhs.shape[0], t.shape[1:]
     out = torch.empty((b, d, f), dtype=torch.float16, device=lhs.device) if out is None else out
-    res = residual if residual is not None else torch.zeros(1, dtype=torch.float16, device=lhs.device)
+    res = residual if residual is not None else _one(lhs, torch.float16)
     bufs = [buffer(x) for x in (lhs, t, bias, norm, res, out)]
     _check(lib().clk_opm_update(_stream(lhs), *map(_ref, bufs), float(eps), int(residual is not None)))
     return out
