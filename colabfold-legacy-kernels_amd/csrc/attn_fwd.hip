@@ -411,10 +411,13 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb) {
                 const float m_new = fmaxf(m_run[qb], wave_xor_max4(m_tile[qb]));
-                const float alpha = exp2_fast((m_run[qb] - m_new) * kLog2e);
-                l_run[qb] *= alpha;
+                // (before the first move l and O are still zero: nothing to rescale)
+                if (m_run[qb] > -INFINITY) {
+                    const float alpha = exp2_fast((m_run[qb] - m_new) * kLog2e);
+                    l_run[qb] *= alpha;
 #pragma unroll
-                for (int db = 0; db < T::kDB; ++db) acc[db][qb] *= alpha;
+                    for (int db = 0; db < T::kDB; ++db) acc[db][qb] *= alpha;
+                }
                 m_run[qb] = m_new;
                 nm2[qb] = -m_new * kLog2e;
                 thr[qb] = m_new * kLog2e + 6.f;
@@ -496,7 +499,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
                     l > 0.f ? m_run[qb] * kLog2e + log2f(l) : -INFINITY;
             }
         }
-        const float inv = 1.0f / fmaxf(l, 1e-30f);
+        const float inv = __builtin_amdgcn_rcpf(fmaxf(l, 1e-30f));
 #pragma unroll
         for (int c = 0; c < DP / 32; ++c) {
             const int d0 = (DP / 4) * g + 8 * c;
