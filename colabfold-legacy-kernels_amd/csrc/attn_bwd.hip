@@ -67,6 +67,7 @@ struct BwdArgs {
     float scale;
     float c1;    // scale log2e, or 1 where |scale log2e| is below 1e-30
     float c1s;   // c1 / log2e: scale, or the stand-in's 1 / log2e
+    float rc1;   // 1 / c1
     int kscale;  // 0 where c1 stands in for a negligible scale: the dK/dV kernel's K is then zero
     int bias_vec;
     int dbias_vec;  // dbias rows are whole 16-byte vectors (Sk % 4 == 0, 16-byte aligned)
@@ -124,9 +125,14 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
     const int64_t qbase = nh * a.Sq * a.D, kbase = nh * a.Sk * a.D;
     const int q0w = qt * T::kBQ + wave * (T::kQB * 16);
 
-    // Q^T and dO^T B operands, lse2 and delta of this lane's queries
+    // Q^T and dO^T B operands, lse2 and delta of this lane's queries: buffer loads over the
+    // (n, h) block of q, dout and out, whose out-of-range slots (past Sq, or d past D) read zeros
     half8 qop[T::kQB][T::kKS], dop[T::kQB][T::kKS];
     float lse2[T::kQB], dlt[T::kQB];
+    const int qrange = __builtin_amdgcn_readfirstlane(a.Sq * a.D * 2);
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.q + qbase), 0, qrange, 0x00020000);
+    const auto rdo = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.dout + qbase), 0, qrange, 0x00020000);
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.out + qbase), 0, qrange, 0x00020000);
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) {
         const int gq = q0w + 16 * qb + r16;
@@ -135,11 +141,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 #pragma unroll
         for (int ks = 0; ks < T::kKS; ++ks) {
             const int d0 = 32 * ks + 8 * g;
-            const bool ok = in && d0 < a.D;
-            const int64_t off = qbase + (int64_t)gq * a.D + d0;
-            qop[qb][ks] = ok ? bld8(a.q + off) : bzero8();
-            dop[qb][ks] = ok ? bld8(a.dout + off) : bzero8();
-            const half8 o = ok ? bld8(a.out + off) : bzero8();
+            const uint32_t voff = in && d0 < a.D ? (uint32_t)(gq * a.D + d0) * 2u : 0x80000000u;
+            qop[qb][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rq, voff, 0, 0));
+            dop[qb][ks] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rdo, voff, 0, 0));
+            const half8 o = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(ro, voff, 0, 0));
 #pragma unroll
             for (int j = 0; j < 8; ++j) part += (float)o[j] * (float)dop[qb][ks][j];
         }
@@ -150,7 +155,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
             // the dK/dV kernel's accumulator inputs: -delta and -lse2 / c1 (past Sq the latter
             // is infinite with the sign that makes c1 times it -inf)
             float* st = a.qstat + (nh * a.SqA + (gq & ~31)) * 2 + (gq & 31);
-            st[0] = (in ? -lse2[qb] : -INFINITY) / a.c1;
+            st[0] = (in ? -lse2[qb] : -INFINITY) * a.rc1;
             st[32] = in ? -dlt[qb] : 0.f;
         }
     }
@@ -1882,6 +1887,7 @@ static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffe
     a.kscale = fabsf(a.c1) >= 1e-30f;
     if (!a.kscale) a.c1 = 1.f;  // scale log2e S is below fp32 resolution against the bias
     a.c1s = a.c1 / kLog2e;
+    a.rc1 = 1.f / a.c1;
     a.bias_vec = Sk % 8 == 0 && aligned16(a.bias);
     a.dbias_vec = Sk % 4 == 0 && aligned16(a.dbias);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);

@@ -260,13 +260,16 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     // parity: loaded one key tile ahead where rows are not whole 16-byte vectors, else read from
     // LDS at the start of the tile (below); when the tile comes up, a masked key's bias becomes
     // the masked logit -1e4 and a key past Sk's -inf
+    // (the register path's row pointers: brow, set where that path starts)
     const half_t* brow[T::kQB];
+    const auto set_brow = [&]() {
 #pragma unroll
-    for (int qb = 0; qb < T::kQB; ++qb) {
-        const int gq = q0w + 16 * qb + r16;
-        const int gqc = gq < a.Sq ? gq : a.Sq - 1;
-        brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
-    }
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const int gq = q0w + 16 * qb + r16;
+            const int gqc = gq < a.Sq ? gq : a.Sq - 1;
+            brow[qb] = a.bias + (int64_t)h * a.Sq * a.Sk + (int64_t)gqc * a.Sk + 16 * g;
+        }
+    };
     // Where bias rows are whole 16-byte vectors (and a head's bias spans under 2^31 bytes) the
     // bias goes through LDS: a lane's 16 keys of one query row are 32 bytes of a different row
     // for each of 16 lanes, so register loads of them touch 16 cache lines per instruction, which
@@ -275,15 +278,16 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     // block, each a contiguous sweep of 8 rows x 128 bytes: lane 8 r + j of load m reads row 8 m + r,
     // 16-byte segment (j - 2 (r / 2)) % 8, and lands at byte 1040 m + 16 (8 r + j) of the wave's
     // buffer. The rotation and the 16-byte skew between loads put the 16 rows of each 16-lane read
-    // on distinct LDS banks. Rows past Sq read row Sq - 1 (their results are never stored); keys
-    // past Sk read the next row's values or zeros and become -inf when their tile comes up.
+    // on distinct LDS banks. Rows past Sq lie past the buffer's range and read zeros (their
+    // results are never stored); keys past Sk read the next row's values or zeros and become -inf
+    // when their tile comes up.
     const half_t* const bias_head = a.bias + (int64_t)h * a.Sq * a.Sk;
     uint32_t bdma[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    {
         const int r = lane >> 3, seg = ((lane & 7) - 2 * (r >> 1)) & 7;
-        const int gq = min(q0w + 8 * m + r, a.Sq - 1);
-        bdma[m] = (uint32_t)gq * (uint32_t)a.Sk * 2u + 16u * (uint32_t)seg;
+        bdma[0] = (uint32_t)(q0w + r) * (uint32_t)a.Sk * 2u + 16u * (uint32_t)seg;
+#pragma unroll
+        for (int m = 1; m < 4; ++m) bdma[m] = bdma[0] + (uint32_t)m * 16u * (uint32_t)a.Sk;
     }
     const auto dma_bias = [&](int k0, int bb) {
         const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(bias_head + k0), 0,
@@ -467,6 +471,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         if constexpr (decltype(vec)::value) {
             dma_bias(0, 0);
         } else {
+            set_brow();
             fetch_bias(0, biasA);
         }
         keep_cur = __ballot(mbyte != 0u);
