@@ -1154,23 +1154,6 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     const bool kin = key < a.Sk;
     const float c1s = a.c1s;
 
-    // the workgroup's bias, fp16: rows kblk 64 .. + 63 and the masked-logit row SkA
-    {
-        constexpr int kFill = (65 * (SqB / 4) + 767) / 768;
-        const float* src = a.biast + (int64_t)h * (a.SkA + 1) * SqB;
-#pragma unroll
-        for (int f = 0; f < kFill; ++f) {
-            const int idx = tid + 768 * f;
-            if (idx < 65 * (SqB / 4)) {
-                const int r = idx / (SqB / 4), c4 = idx - r * (SqB / 4);
-                const int srow = r < 64 ? kblk * 64 + r : a.SkA;
-                const float4 v = *reinterpret_cast<const float4*>(src + (int64_t)srow * SqB + 4 * c4);
-                *reinterpret_cast<half4*>(bias_l + r * kBRow + 4 * c4) =
-                    half4{(half_t)(v.x * (1.f / kLog2e)), (half_t)(v.y * (1.f / kLog2e)),
-                          (half_t)(v.z * (1.f / kLog2e)), (half_t)(v.w * (1.f / kLog2e))};
-            }
-        }
-    }
     if (tid < 192) reinterpret_cast<float4*>(tid < 96 ? qterms0 + 512 : qterms1 + 128)[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // this wave's staging share of a step: tile (third sq3, tile si) of tensor (Q, dO)
@@ -1238,6 +1221,24 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     if (rows > 0) {
         fetch_kv(0);
         dma_s(0, 0, 0);
+    }
+    // (after the first step's loads are issued, so that their latency and the bias loads' overlap)
+    // the workgroup's bias, fp16: rows kblk 64 .. + 63 and the masked-logit row SkA
+    {
+        constexpr int kFill = (65 * (SqB / 4) + 767) / 768;
+        const float* src = a.biast + (int64_t)h * (a.SkA + 1) * SqB;
+#pragma unroll
+        for (int f = 0; f < kFill; ++f) {
+            const int idx = tid + 768 * f;
+            if (idx < 65 * (SqB / 4)) {
+                const int r = idx / (SqB / 4), c4 = idx - r * (SqB / 4);
+                const int srow = r < 64 ? kblk * 64 + r : a.SkA;
+                const float4 v = *reinterpret_cast<const float4*>(src + (int64_t)srow * SqB + 4 * c4);
+                *reinterpret_cast<half4*>(bias_l + r * kBRow + 4 * c4) =
+                    half4{(half_t)(v.x * (1.f / kLog2e)), (half_t)(v.y * (1.f / kLog2e)),
+                          (half_t)(v.z * (1.f / kLog2e)), (half_t)(v.w * (1.f / kLog2e))};
+            }
+        }
     }
     __syncthreads();
 
