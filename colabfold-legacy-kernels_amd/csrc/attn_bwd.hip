@@ -133,6 +133,8 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
     const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.q + qbase), 0, qrange, 0x00020000);
     const auto rdo = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.dout + qbase), 0, qrange, 0x00020000);
     const auto ro = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.out + qbase), 0, qrange, 0x00020000);
+    // (run after the first key tile's loads are issued, so that their latencies overlap)
+    const auto load_queries = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) {
         const int gq = q0w + 16 * qb + r16;
@@ -159,6 +161,7 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
             st[32] = in ? -dlt[qb] : 0.f;
         }
     }
+    };
 
     float4v acc[T::kDB][T::kQB];
 #pragma unroll
@@ -294,8 +297,6 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
 
     // dP^T starts from -delta (the MFMA accumulator input), so dS = p dP is one multiply
     float4v ndlt[T::kQB];
-#pragma unroll
-    for (int qb = 0; qb < T::kQB; ++qb) ndlt[qb] = float4v{-dlt[qb], -dlt[qb], -dlt[qb], -dlt[qb]};
 
     uint64_t keep_cur = 0u;
     const auto tile = [&](int k0, int buf, BH16 (&bias16)[T::kQB], BH16 (&bias_next)[T::kQB]) {
@@ -383,6 +384,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_b
     if (a.Sk > 0) {
         fetch_kv(0, 0);
         fetch_bias(0, biasA);
+    }
+    load_queries();
+#pragma unroll
+    for (int qb = 0; qb < T::kQB; ++qb) ndlt[qb] = float4v{-dlt[qb], -dlt[qb], -dlt[qb], -dlt[qb]};
+    if (a.Sk > 0) {
         keep_cur = __ballot(mbyte != 0u);
         stage(0, keep_cur);
         __syncthreads();

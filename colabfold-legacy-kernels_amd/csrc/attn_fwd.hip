@@ -132,16 +132,19 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
 
     // Q^T as the B operand of S^T: lane column q = q0w + 16 qb + r16, slots d = 32 ks + 8 g + j
     const int q0w = q0 + wave * (T::kQB * 16);
+    // (loaded after the first key tile's loads are issued, so that their latencies overlap)
     half8 qop[T::kQB][T::kKS];
+    const auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int qb = 0; qb < T::kQB; ++qb) {
-        const int gq = q0w + 16 * qb + r16;
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const int gq = q0w + 16 * qb + r16;
 #pragma unroll
-        for (int ks = 0; ks < T::kKS; ++ks) {
-            const int d0 = 32 * ks + 8 * g;
-            qop[qb][ks] = (gq < a.Sq && d0 < a.D) ? ld8(a.q + qbase + gq * a.qs + d0) : zero8();
+            for (int ks = 0; ks < T::kKS; ++ks) {
+                const int d0 = 32 * ks + 8 * g;
+                qop[qb][ks] = (gq < a.Sq && d0 < a.D) ? ld8(a.q + qbase + gq * a.qs + d0) : zero8();
+            }
         }
-    }
+    };
 
     // running max m, its exp2-domain negative -m log2e and raise threshold m log2e + 6, and l
     float m_run[T::kQB], nm2[T::kQB], thr[T::kQB], l_run[T::kQB];
@@ -474,6 +477,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             set_brow();
             fetch_bias(0, biasA);
         }
+        load_q();
         keep_cur = __ballot(mbyte != 0u);
         stage(0, keep_cur);
         __syncthreads();
