@@ -962,15 +962,19 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
     };
 
     // K and V of the next row as B operands (lane column = key, slots d = 8 g + j), its mask byte
+    // the lane's K/V chunk and mask byte of a row: buffer loads from the row's (scalar) base at
+    // offsets fixed for the kernel
     half8 kopn, vopn;
     uint32_t mbn = 0u;
+    const uint32_t kvoff = (uint32_t)((kin ? key : 0) * DP + 8 * g) * 2u, moff = (uint32_t)(kin ? key : 0);
     const auto fetch_kv = [&](int pass) {
         const int64_t nh = row_nh(pass);
-        const int kc = kin ? key : 0;
-        mbn = (uint32_t)a.kmask[(int64_t)row_n(pass) * a.Sk + kc];
-        const int64_t off = (nh * a.Sk + kc) * DP + 8 * g;
-        kopn = bld8(a.k + off);
-        vopn = bld8(a.v + off);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.k + nh * a.Sk * DP), 0, a.Sk * DP * 2, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.v + nh * a.Sk * DP), 0, a.Sk * DP * 2, 0x00020000);
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.kmask + (int64_t)row_n(pass) * a.Sk), 0, a.Sk, 0x00020000);
+        mbn = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, moff, 0, 0);
+        kopn = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, kvoff, 0, 0));
+        vopn = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, kvoff, 0, 0));
     };
 
     float dbias[HT][8];
@@ -1205,15 +1209,19 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
         }
     };
 
+    // the lane's K/V chunk and mask byte of a row: buffer loads from the row's (scalar) base at
+    // offsets fixed for the kernel
     half8 kopn, vopn;
     uint32_t mbn = 0u;
+    const uint32_t kvoff = (uint32_t)((kin ? key : 0) * DP + 8 * g) * 2u, moff = (uint32_t)(kin ? key : 0);
     const auto fetch_kv = [&](int pass) {
         const int64_t nh = row_nh(pass);
-        const int kc = kin ? key : 0;
-        mbn = (uint32_t)a.kmask[(int64_t)row_n(pass) * a.Sk + kc];
-        const int64_t off = (nh * a.Sk + kc) * DP + 8 * g;
-        kopn = bld8(a.k + off);
-        vopn = bld8(a.v + off);
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.k + nh * a.Sk * DP), 0, a.Sk * DP * 2, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.v + nh * a.Sk * DP), 0, a.Sk * DP * 2, 0x00020000);
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.kmask + (int64_t)row_n(pass) * a.Sk), 0, a.Sk, 0x00020000);
+        mbn = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rm, moff, 0, 0);
+        kopn = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, kvoff, 0, 0));
+        vopn = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, kvoff, 0, 0));
     };
 
     float dbias[TT][8];
