@@ -429,7 +429,7 @@ def time_calls(torch, calls, iters, warmup):
     return ms
 
 
-def bench_fused(torch, hip, ev, iters, warmup):
+def bench_fused(torch, hip, iters, warmup):
     M = 262144
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
@@ -674,7 +674,7 @@ def main():
     if not args.no_packed:
         line["packed_fwd"] = bench_packed(torch, hip, args.steps, args.warmup, ev)
     if not args.no_fused:
-        line["fused"] = bench_fused(torch, hip, ev, args.steps, args.warmup)
+        line["fused"] = bench_fused(torch, hip, args.steps, args.warmup)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(line), flush=True)
