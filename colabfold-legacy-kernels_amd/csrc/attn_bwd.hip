@@ -94,7 +94,8 @@ struct BH16 {
 // ------------------------------------------------------------------------------------------
 template <int DP>
 struct DqTile {
-    static constexpr int kWaves = 4, kThreads = kWaves * kWave, kQB = 2;
+    // at D <= 32 one 16-query block per wave (86 VGPRs: five waves per SIMD), else two
+    static constexpr int kWaves = 4, kThreads = kWaves * kWave, kQB = DP == 32 ? 1 : 2;
     static constexpr int kBQ = kWaves * kQB * 16, kBK = 64;
     static constexpr int kKS = DP / 32, kDB = DP / 16;
     static constexpr int kLd = DP + 8;
@@ -102,9 +103,11 @@ struct DqTile {
     static constexpr int kCPT = (kChunks + kThreads - 1) / kThreads;
 };
 
-// At D = 32 three waves per SIMD (at most 168 VGPRs, a few spilled) measured faster than two.
+// At D = 32 one query block per wave fits 86 VGPRs (five waves per SIMD), which measured 1-3%
+// faster than two blocks at three waves per SIMD (142 VGPRs); four waves per workgroup (eight,
+// sharing each key tile, measured 16% slower).
 template <int DP>
-__global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_bwd_dq_kernel(BwdArgs a) {
     using T = DqTile<DP>;
     // two key tiles in flight: one being read by the MFMAs, the next being written
     // (at DP = 32 four unpadded arrays instead, one per tensor and buffer: below)
@@ -1699,7 +1702,9 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
     const int64_t gb = (int64_t)(a.SqB / 32) * p.kblocks * a.H;
     hipLaunchKernelGGL(attn_bwd_biast_kernel, dim3((unsigned)gb), dim3(256), 0, stream, a);
     stage_mark(stream, 1);
-    hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, a);
+    BwdArgs aq = a;
+    aq.fqt = fast_div(qt);  // the dQ kernel's query tiles per (n, h), at its DP's tile height
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<DP>, dim3((unsigned)g1), dim3(Q::kThreads), 0, stream, aq);
     stage_mark(stream, 2);
     if (p.QT > 0) {
         if constexpr (DP == 32) {
@@ -1890,7 +1895,6 @@ static int attention_bwd_impl(clk_stream stream, int32_t device, const clk_buffe
     a.kblocks = p.kblocks;
     a.chunk = p.chunk;
     a.chunks = p.chunks;
-    a.fqt = fast_div((Sq + DqTile<32>::kBQ - 1) / DqTile<32>::kBQ);  // kBQ is the same at every DP
     a.fn = fast_div(N);
     a.fkb = fast_div(p.kblocks);
     a.fch = fast_div(p.chunks);
