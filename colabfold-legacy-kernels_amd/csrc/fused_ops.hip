@@ -1036,218 +1036,215 @@ struct EpiArgs {
     float eps;
 };
 
-// LDS of the tri-mul epilogue: both weights, the two operand tiles, LN parameters, reduction rows
+// A wave's row tile, and the reference's keep unit for this op (cuda/volta_gdp.h:41), which two
+// consecutive tiles share
+constexpr int kEpiRows = 16;
+constexpr int kEpiKeepRows = 32;
+
+// LDS of the tri-mul epilogue: both weights, the LayerNorm parameters and the two bias vectors
 constexpr size_t epi_lds_bytes(int C, int CA, int O) {
-    return (size_t)(O * C + O * CA + kTileRows * C + kTileRows * CA) * 2 +
-           (size_t)(2 * C + 2 * CA + (kEpiThreads / kTileRows) * kTileRows) * 4;
+    return (size_t)(O * C + O * CA) * 2 + (size_t)(2 * C + 2 * CA + 2 * O) * 4;
 }
 
-// Waves per SIMD the epilogue is compiled for: 4 (two workgroups per CU, at most 128 VGPRs) where
-// LDS allows two workgroups and the shape fits 128 VGPRs without spilling, else 2
-constexpr int epi_waves(int C, int CA, int O, bool ADD) {
-    const int sum = C + CA + O;
-    return epi_lds_bytes(C, CA, O) <= 80 * 1024 && !(ADD && sum >= 256) && sum < 320 ? 4 : 2;
-}
 
-// Eight waves; wave w owns column pair w / SPLIT and RBW of the four row blocks. The tile body is
-// straight-line code, so that a wait for a load never waits for the stores issued before it
-// (vmcnt counts loads and stores in issue order, and the compiler's count is that of its weakest
-// path):
-// - the next tile's keep values, x_cm columns, x rows and residual are fetched before this tile's
-//   stores and all waited for (keep decision, both LayerNorms, residual to fp32) in the same
-//   iteration, after the stores, so no fetched register crosses the back edge;
-// - the keep decision of each 32-row half comes from a ballot of the 64 rows (one per lane);
-// - every tile runs both LayerNorms and the GEMMs; padding stores zeros, and the stores of skipped
-//   rows and rows past M are buffer stores at an offset past the tile's end, which the hardware
-//   drops, so no branch skips them.
+// Each wave owns whole 16-row tiles and needs no other wave's data, so the tile loop has no
+// barrier. Lane (r, g) holds row r of the tile, channels 32 ks + 8 g .. +7 of every contraction
+// step ks: exactly the B operand of out^T = W Y^T, so both LayerNorms run in registers (a row's
+// statistics summed over its four lanes by two xor shuffles) and write their fp16 output straight
+// into the MFMA operands. The paired weight blocks in LDS give the lane 8 consecutive output
+// columns of a column pair (a 16-byte store); the products start from the biases. Four waves per
+// SIMD (at most 128 VGPRs): the weight reads of one column pair are in flight at a time.
+// - The next tile's x_cm columns, x rows and keep values are fetched after this tile's
+//   LayerNorms, so they are in flight during its products and stores; the loop waits for them
+//   after the stores, so no fetched register crosses the back edge (vmcnt counts loads and stores
+//   in issue order). With add_input the residual is this tile's x row, so the next one is fetched
+//   after the stores.
+// - Keep decisions come from a ballot of the 32 keep values of the tile's keep unit; padding
+//   stores zeros, and the stores of skipped rows and rows past M go to an offset past the tile's
+//   end, which the hardware drops, so no branch skips them.
 template <int C, int CA, int O, bool ADD, bool BF>
-__global__ __launch_bounds__(kEpiThreads, epi_waves(C, CA, O, ADD))
+__global__ __launch_bounds__(kEpiThreads, 4)
 void epilogue_kernel(EpiArgs a) {
-    constexpr int TH = kEpiThreads, KC = C / 32, KA = CA / 32, TW = TH / kWave;
-    constexpr int kSub = 32;  // the reference's keep granularity here (volta_gdp.h:41)
-    constexpr int NPAIRS = O / 32, SPLIT = TW / NPAIRS, RBW = 4 / SPLIT;
-    static_assert(TW % NPAIRS == 0 && 4 % SPLIT == 0, "whole row blocks per wave");
-    // column LayerNorm of x_cm: a thread holds one row's values of one of NQ channel groups
-    constexpr int NQ = TH / kTileRows, CQ = C / NQ;
-    static_assert(CQ % 8 == 0, "channel groups are whole 16-byte fragments");
+    constexpr int TW = kEpiThreads / kWave, KC = C / 32, KA = CA / 32, NP = O / 32;
+    static_assert(!ADD || O == CA, "the residual is x itself");
     constexpr uint32_t kDrop = 0x80000000u;  // a store offset past every tile's end
     using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     half_t* Wo = lds;
     half_t* Wg = Wo + O * C;
-    half_t* Yf = Wg + O * CA;
-    half_t* Af = Yf + kTileRows * C;
-    float* lsc = reinterpret_cast<float*>(Af + kTileRows * CA);
+    float* lsc = reinterpret_cast<float*>(Wg + O * CA);
     float* lof = lsc + C;
     float* isc = lof + C;
     float* iof = isc + CA;
-    float* red = iof + CA;  // [NQ][64]
+    float* bov = iof + CA;
+    float* bgv = bov + O;
     load_weight_frags<C, true>(Wo, a.woT, O, O / 16);
     load_weight_frags<CA, true>(Wg, a.wgT, O, O / 16);
-    for (int i = threadIdx.x; i < C; i += TH) {
+    for (int i = threadIdx.x; i < C; i += kEpiThreads) {
         lsc[i] = a.ln_scale[i];
         lof[i] = a.ln_offset[i];
     }
-    for (int i = threadIdx.x; i < CA; i += TH) {
+    for (int i = threadIdx.x; i < CA; i += kEpiThreads) {
         isc[i] = a.in_scale[i];
         iof[i] = a.in_offset[i];
+    }
+    for (int i = threadIdx.x; i < O; i += kEpiThreads) {
+        bov[i] = (float)a.bo[i];
+        bgv[i] = (float)a.bg[i];
     }
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int r16 = lane & 15, g = lane >> 4;
-    const int cp = wave / SPLIT, rb0 = (wave % SPLIT) * RBW;
-    const int col = 32 * cp + 8 * g;
-    const int tiles = (a.M + kTileRows - 1) / kTileRows;
-    const int G = gridDim.x;
-    const int r = threadIdx.x % kTileRows, cq = threadIdx.x / kTileRows;
+    // the lane's LayerNorm parameters and biases, all at constant offsets from one address
+    const float* prm = lsc + 8 * g;
+    const int tiles = (a.M + kEpiRows - 1) / kEpiRows;
+    const int stride = gridDim.x * TW;
     const bool has_keep = a.keep != nullptr;
     // without a keep the descriptor has no bytes, and its loads return zeros without touching memory
     const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.keep), 0,
                                                      has_keep ? (uint32_t)a.M * 2u : 0u, 0x00020000);
 
-    float bov[8], bgv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        bov[j] = (float)a.bo[col + j];
-        bgv[j] = (float)a.bg[col + j];
-    }
-
-    // tile t's keep value of row m0 + lane, x_cm values, x rows and residual (rows past M repeat
-    // row M - 1; their results are dropped)
+    // tile t's keep values (row m0k + lane % 32 of its keep unit), x_cm values and x row (rows
+    // past M repeat row M - 1; their results are dropped)
     unsigned short kraw;
-    float v[CQ];
-    RowTile<CA, kTileRows, TH> xt;
-    half8 xa[RBW];
-    const auto fetch = [&](int t) {
-        const int m0 = t * kTileRows;
-        kraw = __builtin_amdgcn_raw_buffer_load_b16(rk, (uint32_t)min(m0 + lane, a.M - 1) * 2u, 0, 0);
-        const int mr = min(m0 + r, a.M - 1);
+    float v[KC][8];
+    half8 xr[KA];
+    const auto fetch_cm = [&](int t) {
+        const int m0 = t * kEpiRows, m0k = m0 & ~(kEpiKeepRows - 1);
+        kraw = __builtin_amdgcn_raw_buffer_load_b16(rk, (uint32_t)min(m0k + (lane & 31), a.M - 1) * 2u, 0, 0);
+        const float* pc = a.x_cm + (int64_t)(8 * g) * a.M + min(m0 + r16, a.M - 1);
 #pragma unroll
-        for (int i = 0; i < CQ; ++i) v[i] = a.x_cm[(int64_t)(cq * CQ + i) * a.M + mr];
-        constexpr int TPR = RowTile<CA, kTileRows, TH>::kTPR;
-        const int row = threadIdx.x / TPR, part = threadIdx.x % TPR;
-        const int mx = min(m0 + row, a.M - 1);
+        for (int ks = 0; ks < KC; ++ks)
 #pragma unroll
-        for (int j = 0; j < RowTile<CA, kTileRows, TH>::kChunks; ++j)
-            xt.v[j] = fld8(a.x + (int64_t)mx * CA + 8 * (part + TPR * j));
-        if constexpr (ADD) {
-#pragma unroll
-            for (int i = 0; i < RBW; ++i)
-                xa[i] = fld8(a.x + (int64_t)min(m0 + 16 * (rb0 + i) + r16, a.M - 1) * CA + col);
-        }
+            for (int e = 0; e < 8; ++e) v[ks][e] = pc[(int64_t)(32 * ks + e) * a.M];
     };
-    // per 32-row half: compute, padding or skip (rows past M count as -1, volta_gdp.h:114-136)
-    int w0 = kCompute, w1 = kCompute;
-    float res[RBW][8];
+    const auto fetch_x = [&](int t) {
+        const half_t* px = a.x + (int64_t)min(t * kEpiRows + r16, a.M - 1) * CA + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < KA; ++ks) xr[ks] = fld8(px + 32 * ks);
+    };
+    // the keep decision and both LayerNorms of tile t into the MFMA operands
+    int work = kCompute;
+    half8 yf[KC], af[KA];
     const auto prepare = [&](int t) {
-        const int m0 = t * kTileRows;
-        const float k = m0 + lane < a.M ? (has_keep ? (float)__builtin_bit_cast(half_t, kraw) : 1.f) : -1.f;
-        const uint64_t live = __ballot(k > 0.f), zero = __ballot(k == 0.f);
-        const uint32_t live0 = (uint32_t)live, live1 = (uint32_t)(live >> 32);
-        const uint32_t zero0 = (uint32_t)zero, zero1 = (uint32_t)(zero >> 32);
-        w0 = live0 ? (int)kCompute : zero0 ? (int)kPadding : (int)kSkip;
-        w1 = live1 ? (int)kCompute : zero1 ? (int)kPadding : (int)kSkip;
-        float s = 0.f;
+        const int m0k = (t * kEpiRows) & ~(kEpiKeepRows - 1);
+        const float k = m0k + (lane & 31) < a.M ? (has_keep ? (float)__builtin_bit_cast(half_t, kraw) : 1.f) : -1.f;
+        const uint32_t live = (uint32_t)__ballot(k > 0.f), zero = (uint32_t)__ballot(k == 0.f);
+        work = live ? (int)kCompute : zero ? (int)kPadding : (int)kSkip;
+        {
+            float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < CQ; ++i) s += v[i];
-        __syncthreads();  // the previous tile's operand and reduction reads are done
-        red[cq * kTileRows + r] = s;
-        __syncthreads();
-        float mean = 0.f;
+            for (int ks = 0; ks < KC; ++ks)
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) mean += red[q * kTileRows + r];
-        mean *= 1.f / C;
-        float q2 = 0.f;
-        float d[CQ];
+                for (int e = 0; e < 8; ++e) s += v[ks][e];
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            const float mean = s * (1.f / C);
+            float q = 0.f;
 #pragma unroll
-        for (int i = 0; i < CQ; ++i) {
-            d[i] = v[i] - mean;
-            q2 += d[i] * d[i];
+            for (int ks = 0; ks < KC; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    v[ks][e] -= mean;
+                    q += v[ks][e] * v[ks][e];
+                }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rstd = __builtin_amdgcn_rsqf(q * (1.f / C) + a.eps);
+#pragma unroll
+            for (int ks = 0; ks < KC; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    yf[ks][e] = (half_t)(v[ks][e] * rstd * prm[32 * ks + e] + prm[C + 32 * ks + e]);
         }
-        __syncthreads();
-        red[cq * kTileRows + r] = q2;
-        __syncthreads();
-        float var = 0.f;
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) var += red[q * kTileRows + r];
-        const float rstd = __builtin_amdgcn_rsqf(var * (1.f / C) + a.eps);
+            for (int ks = 0; ks < KA; ++ks)
 #pragma unroll
-        for (int i = 0; i < CQ; i += 8) {
-            half8 y;
+                for (int e = 0; e < 8; ++e) s += act_get<BF>(xr[ks], e);
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            const float mean = s * (1.f / CA);
+            float q = 0.f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int c = cq * CQ + i + e;
-                y[e] = (half_t)(d[i + e] * rstd * lsc[c] + lof[c]);
-            }
-            const int c = (cq * CQ + i) / 8;
-            fst8(Yf + frag(r >> 4, c >> 2, KC, (r & 15) + 16 * (c & 3)), y);
+            for (int ks = 0; ks < KA; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = act_get<BF>(xr[ks], e) - mean;
+                    q += d * d;
+                }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rstd = __builtin_amdgcn_rsqf(q * (1.f / CA) + a.eps);
+#pragma unroll
+            for (int ks = 0; ks < KA; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    af[ks][e] = (half_t)((act_get<BF>(xr[ks], e) - mean) * rstd * prm[2 * C + 32 * ks + e] +
+                                         prm[2 * C + CA + 32 * ks + e]);
         }
-        ln_rows_to_frags<CA, kTileRows, false, true, TH, BF>(Af, xt, isc, iof, a.eps);
-#pragma unroll
-        for (int i = 0; i < RBW; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) res[i][j] = ADD ? pin_f32(act_get<BF>(xa[i], j)) : 0.f;  // here, not after the next fetch
-        __syncthreads();
     };
     const auto gemm_store = [&](int t) {
-        const int m0 = t * kTileRows;
-        float4v ao[2][RBW], ag[2][RBW];
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-            for (int i = 0; i < RBW; ++i) {
-                ao[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
-                ag[hb][i] = float4v{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-        for (int ks = 0; ks < KC; ++ks) {
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const half8 w = fld8(Wo + frag(2 * cp + hb, ks, KC, lane));
-#pragma unroll
-                for (int i = 0; i < RBW; ++i)
-                    ao[hb][i] = mfma16x16x32(w, fld8(Yf + frag(rb0 + i, ks, KC, lane)), ao[hb][i]);
-            }
-        }
-#pragma unroll
-        for (int ks = 0; ks < KA; ++ks) {
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-                const half8 w = fld8(Wg + frag(2 * cp + hb, ks, KA, lane));
-#pragma unroll
-                for (int i = 0; i < RBW; ++i)
-                    ag[hb][i] = mfma16x16x32(w, fld8(Af + frag(rb0 + i, ks, KA, lane)), ag[hb][i]);
-            }
-        }
+        const int m0 = t * kEpiRows;
         // the tile's rows as one buffer: rows past M lie past its end
-        const uint32_t rows = (uint32_t)min(kTileRows, a.M - m0);
+        const uint32_t rows = (uint32_t)min(kEpiRows, a.M - m0);
         const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.out + (int64_t)m0 * O, 0, rows * O * 2u, 0x00020000);
+        const bool store = work == kCompute || (!ADD && work == kPadding);
 #pragma unroll
-        for (int i = 0; i < RBW; ++i) {
-            const int rb = rb0 + i;
-            const int w = 16 * rb < kSub ? w0 : w1;
-            const bool store = w == kCompute || (!ADD && w == kPadding);
-            half8 o;
+        for (int cp = 0; cp < NP; ++cp) {
+            constexpr int kBo = 2 * C + 2 * CA, kBg = kBo + O;  // bov, bgv
+            float4v ao[2], ag[2];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float val = (ao[j >> 2][i][j & 3] + bov[j]) * sigmoid_fast(ag[j >> 2][i][j & 3] + bgv[j]);
-                o[j] = act_cvt<BF>(w == kPadding ? 0.f : val + res[i][j]);
+            for (int hb = 0; hb < 2; ++hb) {
+                ao[hb] = *reinterpret_cast<const float4v*>(prm + kBo + 32 * cp + 4 * hb);
+                ag[hb] = *reinterpret_cast<const float4v*>(prm + kBg + 32 * cp + 4 * hb);
             }
-            const uint32_t off = (uint32_t)((16 * rb + r16) * O + col) * 2u;
+#pragma unroll
+            for (int ks = 0; ks < KC; ++ks)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb)
+                    ao[hb] = mfma16x16x32(fld8(Wo + frag(2 * cp + hb, ks, KC, lane)), yf[ks], ao[hb]);
+#pragma unroll
+            for (int ks = 0; ks < KA; ++ks)
+#pragma unroll
+                for (int hb = 0; hb < 2; ++hb)
+                    ag[hb] = mfma16x16x32(fld8(Wg + frag(2 * cp + hb, ks, KA, lane)), af[ks], ag[hb]);
+            const int col = 32 * cp + 8 * g;
+            half8 o;
+            if (work == kPadding) {
+                o = fzero8();
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float val = ao[j >> 2][j & 3] * sigmoid_fast(ag[j >> 2][j & 3]);
+                    const float res = ADD ? pin_f32(act_get<BF>(xr[cp], j)) : 0.f;
+                    o[j] = act_cvt<BF>(val + res);
+                }
+            }
+            const uint32_t off = (uint32_t)(r16 * O + col) * 2u;
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
+            // one column pair's weight reads in flight at a time (hoisting them all costs registers)
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    int t = blockIdx.x;
+    // With add_input the residual is this tile's x row, so the next tile's x row is fetched only
+    // after this tile's stores (the output aliases x, but the next tile's rows are not this one's).
+    int t = blockIdx.x * TW + wave;
+    fetch_cm(min(t, tiles - 1));
+    fetch_x(min(t, tiles - 1));
+    __syncthreads();  // the weights, LayerNorm parameters and biases are in LDS
     if (t >= tiles) return;
-    fetch(t);
     prepare(t);
     for (;;) {
-        const int nt = t + G;
-        // with add_input the output aliases x: the next tile's rows are not this tile's
-        fetch(min(nt, tiles - 1));
+        const int nt = t + stride;
+        fetch_cm(min(nt, tiles - 1));
+        if constexpr (!ADD) fetch_x(min(nt, tiles - 1));
         gemm_store(t);
         if (nt >= tiles) break;
+        if constexpr (ADD) fetch_x(nt);
         t = nt;
         prepare(t);
     }
@@ -1711,9 +1708,10 @@ template <int C, int CA, int O, bool ADD, bool BF>
 static int run_epilogue(const EpiArgs& a, hipStream_t s) {
     constexpr int TH = kEpiThreads;
     constexpr size_t lds = epi_lds_bytes(C, CA, O);
-    const int64_t tiles = (a.M + kTileRows - 1) / kTileRows;
-    // as many workgroups per CU as the registers the kernel is compiled for allow
-    const dim3 grid(persistent_grid(tiles, lds, epi_waves(C, CA, O, ADD) / 2));
+    // one 32-row tile per wave at a time; as many workgroups per CU as the registers the kernel is
+    // compiled for allow
+    const int64_t groups = ((a.M + kEpiRows - 1) / kEpiRows + TH / kWave - 1) / (TH / kWave);
+    const dim3 grid(persistent_grid(groups, lds, 4 * 4 / (TH / kWave)));
     if (int st = launch_fused("trimul_epilogue", epilogue_kernel<C, CA, O, ADD, BF>, grid, lds, s, &a, 0)) return st;
     stage_mark(s, 0);
     hipLaunchKernelGGL((epilogue_kernel<C, CA, O, ADD, BF>), grid, dim3(TH), lds, s, a);
@@ -1723,8 +1721,8 @@ static int run_epilogue(const EpiArgs& a, hipStream_t s) {
 
 template <int C, int CA, bool BF>
 static int epilogue_dispatch_o(const EpiArgs& a, bool add, hipStream_t s) {
-    if (a.O == 64) return add ? run_epilogue<C, CA, 64, true, BF>(a, s) : run_epilogue<C, CA, 64, false, BF>(a, s);
-    return add ? run_epilogue<C, CA, 128, true, BF>(a, s) : run_epilogue<C, CA, 128, false, BF>(a, s);
+    if (add) return run_epilogue<C, CA, CA, true, BF>(a, s);  // add_input implies O == CA (checked above)
+    return a.O == 64 ? run_epilogue<C, CA, 64, false, BF>(a, s) : run_epilogue<C, CA, 128, false, BF>(a, s);
 }
 
 template <int C, bool BF>
