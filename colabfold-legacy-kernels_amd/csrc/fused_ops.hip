@@ -1571,6 +1571,186 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
     if constexpr (DB) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// The transition at C = 64, where both weights fit in LDS at once (W1 [H][64] and W2 [64][H], at
+// most 64 KB): one workgroup of 16 waves per CU holds them for the whole call, and each wave owns
+// whole 32-row tiles (two 16-row blocks), so the tile loop has no barrier. As in the tri-mul
+// epilogue, lane (r, g) loads exactly its B-operand slots of x (row r of each block, channels
+// 32 ks + 8 g .. +7), runs the LayerNorm in registers (a row's statistics over its four lanes by two
+// xor shuffles) and keeps the fp16 result as the first product's operand. The hidden units go 32
+// at a time: two paired W1 blocks give the lane hidden units 32 p + 8 g .. +7 of its rows, which
+// after bias, relu and rounding to fp16 are exactly its B operand of the second product's step p,
+// so the hidden activation never leaves registers. Every weight fragment read feeds both blocks.
+// - The next tile's x rows and keep values are fetched after this tile's LayerNorm (with
+//   add_input, whose residual is this tile's x, after its stores), so no fetched register crosses
+//   the back edge (vmcnt counts loads and stores in issue order).
+// - Keep decisions come from a ballot of the 64 keep values of the tile's keep unit (64 rows at
+//   C = 64, cuda/volta_ops.cu:551-553); padding stores zeros, and the stores of skipped rows and
+//   rows past M go to an offset past the tile's end, which the hardware drops.
+constexpr int kTransRowsThreads = 1024;
+constexpr int kTransRowsTile = 32;
+constexpr size_t trans_rows_lds_bytes(int C, int H) { return (size_t)2 * H * C * 2 + (size_t)(3 * C + H) * 4; }
+
+template <bool ADD, bool BF>
+__global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(TransArgs a) {
+    constexpr int C = 64, KS = C / 32, NCB = C / 16, RB = kTransRowsTile / 16, TW = kTransRowsThreads / kWave;
+    constexpr int kKeep = TransTile<C>::kSub;
+    constexpr uint32_t kDrop = 0x80000000u;  // a store offset past every tile's end
+    using u32x4 = unsigned int __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    const int H = a.H, KH = H / 32;
+    half_t* W1 = lds;          // [H/16 paired blocks][KS][64 lanes][8]
+    half_t* W2 = W1 + H * C;   // [C/16 paired blocks][KH][64 lanes][8]
+    float* sc = reinterpret_cast<float*>(W2 + H * C);
+    float* of = sc + C;
+    float* b2s = of + C;
+    float* b1s = b2s + C;  // [H]
+    load_weight_frags<C, true>(W1, a.w1T, H, H / 16);
+    // W2 operand block cb, step p: output channels pair_row(cb, r), hidden 32 p + 8 g .. +7, from
+    // the blocked w2T [H/64][C][64]
+    for (int i = threadIdx.x; i < NCB * KH * kWave; i += kTransRowsThreads) {
+        const int l = i % kWave, t = i / kWave, p = t % KH, cb = t / KH;
+        const int c = pair_row(cb, l & 15);
+        fst8(W2 + i * 8, fld8(a.w2T + ((int64_t)(p >> 1) * C + c) * kHid + 32 * (p & 1) + 8 * (l >> 4)));
+    }
+    for (int i = threadIdx.x; i < C; i += kTransRowsThreads) {
+        sc[i] = a.scale[i];
+        of[i] = a.offset[i];
+        b2s[i] = a.b2[i];
+    }
+    for (int i = threadIdx.x; i < H; i += kTransRowsThreads) b1s[i] = a.b1[i];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int tiles = (a.M + kTransRowsTile - 1) / kTransRowsTile;
+    const int stride = gridDim.x * TW;
+    const bool has_keep = a.keep != nullptr;
+    // without a keep the descriptor has no bytes, and its loads return zeros without touching memory
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.keep), 0,
+                                                     has_keep ? (uint32_t)a.M * 2u : 0u, 0x00020000);
+
+    // tile t's keep values (row m0k + lane of its keep unit) and x rows (rows past M repeat row
+    // M - 1; their results are dropped)
+    unsigned short kraw;
+    half8 xr[RB][KS];
+    const auto fetch = [&](int t) {
+        const int m0 = t * kTransRowsTile, m0k = m0 & ~(kKeep - 1);
+        kraw = __builtin_amdgcn_raw_buffer_load_b16(rk, (uint32_t)min(m0k + lane, a.M - 1) * 2u, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const half_t* px = a.x + (int64_t)min(m0 + 16 * rb + r16, a.M - 1) * C + 8 * g;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xr[rb][ks] = fld8(px + 32 * ks);
+        }
+    };
+    int work = kCompute;
+    half8 yf[RB][KS];
+    const auto prepare = [&](int t) {
+        const int m0k = (t * kTransRowsTile) & ~(kKeep - 1);
+        const float k = m0k + lane < a.M ? (has_keep ? (float)__builtin_bit_cast(half_t, kraw) : 1.f) : -1.f;
+        const uint64_t live = __ballot(k > 0.f), zero = __ballot(k == 0.f);
+        work = live ? (int)kCompute : zero ? (int)kPadding : (int)kSkip;
+        const float* prm = sc + 8 * g;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            float s = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s += act_get<BF>(xr[rb][ks], e);
+            s += __shfl_xor(s, 16);
+            s += __shfl_xor(s, 32);
+            const float mean = s * (1.f / C);
+            float q = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float d = act_get<BF>(xr[rb][ks], e) - mean;
+                    q += d * d;
+                }
+            q += __shfl_xor(q, 16);
+            q += __shfl_xor(q, 32);
+            const float rstd = __builtin_amdgcn_rsqf(q * (1.f / C) + a.eps);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    yf[rb][ks][e] = (half_t)((act_get<BF>(xr[rb][ks], e) - mean) * rstd * prm[32 * ks + e] +
+                                             prm[C + 32 * ks + e]);
+        }
+    };
+    const auto gemm_store = [&](int t) {
+        float4v acc[NCB][RB];
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+        const float* b1l = b1s + 8 * g;
+        for (int p = 0; p < KH; ++p) {
+            float4v hacc[2][RB];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) hacc[h2][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    const half8 w = fld8(W1 + frag(2 * p + h2, ks, KS, lane));
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) hacc[h2][rb] = mfma16x16x32(w, yf[rb][ks], hacc[h2][rb]);
+                }
+            // relu(. + b1), fp16: slot 8 g + e of step p is hidden unit 32 p + 8 g + e
+            half8 hop[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    hop[rb][e] = (half_t)fmaxf(hacc[e >> 2][rb][e & 3] + b1l[32 * p + e], 0.f);
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                const half8 w = fld8(W2 + frag(cb, p, KH, lane));
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = mfma16x16x32(w, hop[rb], acc[cb][rb]);
+            }
+        }
+        // lane: channels 32 cp + 8 g .. +7 of rows m0 + 16 rb + r16
+        const int m0 = t * kTransRowsTile;
+        const uint32_t rows = (uint32_t)min(kTransRowsTile, a.M - m0);
+        const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.out + (int64_t)m0 * C, 0, rows * C * 2u, 0x00020000);
+        const bool store = work == kCompute || (!ADD && work == kPadding);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cp = 0; cp < NCB / 2; ++cp) {
+                const int col = 32 * cp + 8 * g;
+                half8 o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float res = ADD ? act_get<BF>(xr[rb][cp], e) : 0.f;
+                    o[e] = act_cvt<BF>(work == kPadding ? 0.f : acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + res);
+                }
+                const uint32_t off = (uint32_t)((16 * rb + r16) * C + col) * 2u;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
+            }
+    };
+
+    int t = blockIdx.x * TW + wave;
+    fetch(min(t, tiles - 1));
+    __syncthreads();  // the weights, LayerNorm parameters and biases are in LDS
+    if (t >= tiles) return;
+    prepare(t);
+    for (;;) {
+        const int nt = t + stride;
+        if constexpr (!ADD) fetch(min(nt, tiles - 1));
+        gemm_store(t);
+        if (nt >= tiles) break;
+        if constexpr (ADD) fetch(nt);
+        t = nt;
+        prepare(t);
+    }
+}
+
 // ---- host side --------------------------------------------------------------------------------
 
 static int fused_cu_count() {
@@ -1934,8 +2114,26 @@ extern "C" int clk_output_projection(clk_stream stream, const clk_buffer* o, con
     return invalid("output_projection: K and N must be 64 or 128");
 }
 
+template <bool ADD, bool BF>
+static int run_transition_rows(const TransArgs& a, hipStream_t s) {
+    const size_t lds = trans_rows_lds_bytes(64, a.H);
+    const int64_t groups = ((a.M + kTransRowsTile - 1) / kTransRowsTile + kTransRowsThreads / kWave - 1) /
+                           (kTransRowsThreads / kWave);
+    const dim3 grid(persistent_grid(groups, lds, 1));
+    if (int st = launch_fused("transition", transition_rows_kernel<ADD, BF>, grid, lds, s, &a, 0)) return st;
+    stage_mark(s, 0);
+    hipLaunchKernelGGL((transition_rows_kernel<ADD, BF>), grid, dim3(kTransRowsThreads), lds, s, a);
+    stage_mark(s, 1);
+    return launch_status("transition");
+}
+
 template <int C, bool ADD, bool BF>
 static int run_transition(const TransArgs& a, hipStream_t s) {
+    if constexpr (C == 64) {
+        // both weights resident in LDS (at most 66 KB at H = 4C)
+        const int limit = fused_lds_limit();
+        if (limit <= 0 || trans_rows_lds_bytes(64, a.H) <= (size_t)limit) return run_transition_rows<ADD, BF>(a, s);
+    }
     using T = TransTile<C>;
     constexpr int TH = trans_threads(C);
     constexpr int kTR = trans_rows<C>();
