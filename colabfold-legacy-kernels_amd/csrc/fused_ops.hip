@@ -1254,20 +1254,13 @@ void epilogue_kernel(EpiArgs a) {
 //
 // out^T = W2^T relu(W1 X^T + b1) + b2 over hidden chunks of 64: the first product's accumulator
 // (rows = hidden units in pair order) is exactly the B operand of the second, so the hidden
-// activation never leaves registers. Weight chunks stream through LDS and every weight fragment a
-// wave reads feeds one MFMA per 16-row block of its rows: at C = 128 a 256-row tile (two blocks a
-// wave, which halves the LDS weight reads per MFMA: the kernel is bound by them), otherwise 128
-// rows. The biases live in LDS, so no global load is waited for between a chunk's prefetch and
-// its use; the last chunk prefetches the first for the next tile, and at C = 64 (where registers
-// allow) the next tile's rows are fetched during this tile's chunks.
-//
-// At C = 64 the chunks are double-buffered in two LDS arrays and go from memory straight into LDS
-// by direct-to-LDS loads (buffer_load ... lds), issued right after the barrier that opens the
-// previous chunk: one barrier per chunk, no staging registers and no LDS store instructions. The
-// two buffers are separate arrays and the chunk loop is unrolled by two, so each buffer is known
-// at compile time and the compiler can tell that a chunk's weight reads do not alias the loads in
-// flight into the other buffer. Elsewhere a chunk goes through registers into one buffer between
-// two barriers.
+// activation never leaves registers. At C = 128 and 256 the weights do not fit in LDS whole, so
+// 64-unit chunks stream through it (each through registers into one buffer between two barriers)
+// and every weight fragment a wave reads feeds one MFMA per 16-row block of its rows: at C = 128 a
+// 256-row tile (two blocks a wave, which halves the LDS weight reads per MFMA: the kernel is bound
+// by them), at C = 256 128 rows. The biases live in LDS, so no global load is waited for between a
+// chunk's prefetch and its use; the last chunk prefetches the first for the next tile. At C = 64
+// both weights fit in LDS, and transition_rows_kernel below serves that width.
 constexpr int kHid = 64;
 template <int C>
 constexpr int trans_rows() { return C == 128 ? 256 : 128; }
@@ -1292,35 +1285,23 @@ struct TransTile {
     static constexpr int kSub = C > 128 ? 32 : 64;        // keep granularity (volta_ops.cu:551-553)
 };
 
-// Threads per workgroup: at C <= 128 eight waves (of two 16-row blocks each at C = 128, of one at
-// C = 64, where more waves per SIMD hide each other's LDS and MFMA latency better), at C = 256
-// four waves of two row blocks.
-// Workgroups per CU the kernel is compiled for: two at C = 64.
+// Threads per workgroup (one workgroup per CU): at C = 128 eight waves of two 16-row blocks, at
+// C = 256 four waves of two row blocks.
 constexpr int trans_threads(int C) { return C <= 128 ? 512 : 256; }
-constexpr int trans_per_cu(int C) { return C == 64 ? 2 : 1; }
-// Whether the weight chunks are double-buffered by direct-to-LDS loads: at C = 64 (measured 6%
-// faster than register staging); at C = 128 it measured 3% slower, and at C = 256 two chunks do
-// not fit beside the row tile
-constexpr bool trans_double_buffer(int C) { return C == 64; }
 
 template <int C, bool ADD, int TH, bool BF>
-__global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_kernel(TransArgs a) {
+__global__ __launch_bounds__(TH, TH / 256) void transition_kernel(TransArgs a) {
     using T = TransTile<C>;
     constexpr int kTR = trans_rows<C>();
     constexpr int TW = TH / kWave, RB = kTR / 16 / TW, kCPT = T::kChunks / TH;
     static_assert(RB * TW * 16 == kTR && kCPT * TH == T::kChunks, "whole row blocks and chunks");
     constexpr int KS = T::KS, NCB = C / 16, NSUB = kTR / T::kSub;
-    constexpr bool PF = C == 64;
-    constexpr bool DB = trans_double_buffer(C);
-    static_assert(DB || !PF, "the next tile's rows are prefetched on the double-buffered path only");
-    constexpr int kWB = T::kW1 + T::kW2;
-    // the two weight chunk buffers of the direct-to-LDS path
-    __shared__ __attribute__((aligned(16))) half_t WA[DB ? kWB : 8], WB[DB ? kWB : 8];
+    static_assert(C != 64, "C = 64 is transition_rows_kernel's");
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     half_t* Xf = lds;                   // the row tile's LayerNorm output, fragment-major
     half_t* W1 = Xf + kTR * C;          // (C = 256) hidden chunk of w1, then of w2
     half_t* W2 = W1 + T::kW1;
-    float* sc = reinterpret_cast<float*>(DB ? W1 : W2 + T::kW2);
+    float* sc = reinterpret_cast<float*>(W2 + T::kW2);
     float* of = sc + C;
     float* b2s = of + C;
     float* b1s = b2s + C;  // [H]
@@ -1339,21 +1320,10 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
     // weight chunk j: W1 fragments of hidden rows 64 j + pair_row(hb, r), W2 fragments of output
     // channels pair_row(cb, r) over hidden 64 j + 32 kt + 8 g ..; fragment t (of 64 lanes' 16-byte
     // operands) is 16-byte chunks 64 t .. + 63 of the chunk, and thread i stages chunk i
-    const auto w1_offset = [&](int j, int t, int l) __attribute__((always_inline)) -> int64_t {
-        const int ks = t % KS, hb = t / KS;
-        const int hid = kHid * j + pair_row(hb, l & 15);
-        return (int64_t)hid * C + 32 * ks + 8 * (l >> 4);
-    };
-    const auto w2_offset = [&](int j, int t, int l) __attribute__((always_inline)) -> int64_t {
-        const int t2 = t - T::kW1 / (8 * kWave);
-        const int kt = t2 & 1, cb = t2 >> 1;
-        const int c = pair_row(cb, l & 15);
-        return ((int64_t)j * C + c) * kHid + 32 * kt + 8 * (l >> 4);
-    };
-    half8 wreg[DB ? 1 : kCPT];
+    half8 wreg[kCPT];
     const auto fetch_w = [&](int j) {
 #pragma unroll
-        for (int u = 0; u < (DB ? 0 : kCPT); ++u) {
+        for (int u = 0; u < kCPT; ++u) {
             const int i = threadIdx.x + u * TH;
             const int l = i % kWave, t = i / kWave;
             if (i < T::kW1 / 8) {
@@ -1370,34 +1340,11 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
     };
     const auto store_w = [&]() {
 #pragma unroll
-        for (int u = 0; u < (DB ? 0 : kCPT); ++u) fst8(W1 + (threadIdx.x + u * TH) * 8, wreg[u]);
-    };
-    // the direct-to-LDS form: wave w loads fragments w + TW u, each one 1 KB load landing at the
-    // fragment's place (lane l's 16 bytes at byte 16 l); both weights are [H][C] elements
-    const uint32_t wbytes = (uint32_t)a.H * C * 2u;
-    const auto r1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.w1T), 0, wbytes, 0x00020000);
-    const auto r2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.w2T), 0, wbytes, 0x00020000);
-    // (the first kU1 loads of a wave are W1 fragments, the rest W2's)
-    constexpr int kU1 = T::kW1 / (8 * kWave) / TW;
-    static_assert(kU1 * TW * 8 * kWave == T::kW1, "whole W1 loads per wave");
-    const auto dma_w = [&](int j, half_t* dst) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < (DB ? kCPT : 0); ++u) {
-            const int t = wv + TW * u;
-            const uint32_t off = (uint32_t)((u < kU1 ? w1_offset(j, t, lane) : w2_offset(j, t, lane)) * 2);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(u < kU1 ? r1 : r2,
-                                                     (__attribute__((address_space(3))) void*)(dst + t * kWave * 8),
-                                                     16, off, 0, 0, 0);
-        }
+        for (int u = 0; u < kCPT; ++u) fst8(W1 + (threadIdx.x + u * TH) * 8, wreg[u]);
     };
 
     RowTile<C, kTR, TH> xt;
-    if constexpr (DB) {
-        dma_w(0, WA);
-    } else {
-        fetch_w(0);
-    }
-    if (PF && blockIdx.x < tiles) fetch_rows<C, kTR>(xt, a.x, a.M, blockIdx.x * kTR);
+    fetch_w(0);
     for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
         const int m0 = tile * kTR;
         int work[NSUB];
@@ -1415,11 +1362,9 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
                         fst8(a.out + (int64_t)(m0 + r) * C + c, fzero8());
                 }
             }
-            if (PF && tile + (int)gridDim.x < tiles)
-                fetch_rows<C, kTR>(xt, a.x, a.M, (tile + gridDim.x) * kTR);
             continue;
         }
-        if (!PF) fetch_rows<C, kTR>(xt, a.x, a.M, m0);
+        fetch_rows<C, kTR>(xt, a.x, a.M, m0);
         __syncthreads();
         ln_rows_to_frags<C, kTR, false, true, TH, BF>(Xf, xt, sc, of, a.eps);
 
@@ -1429,17 +1374,18 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
         half8 xop[RB][KS];
-        const auto first = [&]() __attribute__((always_inline)) {
+        for (int j = 0; j < chunks; ++j) {
+            __syncthreads();  // the previous chunk's weight reads are done
+            store_w();
+            __syncthreads();
+            if (j == 0) {
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
+                for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(RB * wave + rb, ks, KS, lane));
-            // issued before the weights, so waiting for those (in issue order) covers these
-            if (PF && tile + (int)gridDim.x < tiles)
-                fetch_rows<C, kTR>(xt, a.x, a.M, (tile + gridDim.x) * kTR);
-        };
-        // chunk j's two products from its weights in LDS
-        const auto compute = [&](int j, const half_t* w1s, const half_t* w2s) __attribute__((always_inline)) {
+                    for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(RB * wave + rb, ks, KS, lane));
+            }
+            fetch_w(j + 1 < chunks ? j + 1 : 0);  // the first chunk again for the next tile
+
             // hidden^T for 64 units x this wave's 16 RB rows
             float4v hacc[4][RB];
 #pragma unroll
@@ -1450,12 +1396,11 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int hb = 0; hb < 4; ++hb) {
-                    const half8 w = fld8(w1s + frag(hb, ks, KS, lane));
+                    const half8 w = fld8(W1 + frag(hb, ks, KS, lane));
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) hacc[hb][rb] = mfma16x16x32(w, xop[rb][ks], hacc[hb][rb]);
                 }
             }
-            // relu(. + b1), fp16: slot 8 g + e of step kt is hidden unit 32 kt + 8 g + e
             half8 hop[2][RB];
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
@@ -1472,74 +1417,9 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
             for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt) {
-                    const half8 w = fld8(w2s + frag(cb, kt, 2, lane));
+                    const half8 w = fld8(W2 + frag(cb, kt, 2, lane));
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = mfma16x16x32(w, hop[kt][rb], acc[cb][rb]);
-                }
-            }
-        };
-        if constexpr (DB) {
-            // chunk j from cur while chunk j + 1 (or the next tile's first) loads into nxt: the
-            // wait and barrier that open a chunk cover its loads and the end of the reads of nxt
-            const auto step = [&](int j, half_t* cur, half_t* nxt) __attribute__((always_inline)) {
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                if (j == 0) first();
-                dma_w(j + 1 < chunks ? j + 1 : 0, nxt);
-                compute(j, cur, cur + T::kW1);
-            };
-            for (int j = 0; j < chunks; j += 2) {
-                step(j, WA, WB);
-                step(j + 1, WB, WA);
-            }
-        } else {
-            for (int j = 0; j < chunks; ++j) {
-                __syncthreads();  // the previous chunk's weight reads are done
-                store_w();
-                __syncthreads();
-                if (j == 0) {
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                        for (int ks = 0; ks < KS; ++ks) xop[rb][ks] = fld8(Xf + frag(RB * wave + rb, ks, KS, lane));
-                }
-                fetch_w(j + 1 < chunks ? j + 1 : 0);  // the first chunk again for the next tile
-
-                // hidden^T for 64 units x this wave's 16 RB rows
-                float4v hacc[4][RB];
-#pragma unroll
-                for (int hb = 0; hb < 4; ++hb)
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb) hacc[hb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-                    for (int hb = 0; hb < 4; ++hb) {
-                        const half8 w = fld8(W1 + frag(hb, ks, KS, lane));
-#pragma unroll
-                        for (int rb = 0; rb < RB; ++rb) hacc[hb][rb] = mfma16x16x32(w, xop[rb][ks], hacc[hb][rb]);
-                    }
-                }
-                half8 hop[2][RB];
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
-                    float b1v[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) b1v[e] = b1s[kHid * j + 32 * kt + 8 * g + e];
-#pragma unroll
-                    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                        for (int e = 0; e < 8; ++e)
-                            hop[kt][rb][e] = (half_t)fmaxf(hacc[2 * kt + (e >> 2)][rb][e & 3] + b1v[e], 0.f);
-                }
-#pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) {
-#pragma unroll
-                    for (int kt = 0; kt < 2; ++kt) {
-                        const half8 w = fld8(W2 + frag(cb, kt, 2, lane));
-#pragma unroll
-                        for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = mfma16x16x32(w, hop[kt][rb], acc[cb][rb]);
-                    }
                 }
             }
         }
@@ -1567,8 +1447,6 @@ __global__ __launch_bounds__(TH, trans_per_cu(C) * TH / 256) void transition_ker
             }
         }
     }
-    // the last tile's prefetch of a first chunk (unused) lands before the workgroup's LDS is freed
-    if constexpr (DB) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // The transition at C = 64, where both weights fit in LDS at once (W1 [H][64] and W2 [64][H], at
@@ -2129,31 +2007,29 @@ static int run_transition_rows(const TransArgs& a, hipStream_t s) {
 
 template <int C, bool ADD, bool BF>
 static int run_transition(const TransArgs& a, hipStream_t s) {
-    if constexpr (C == 64) {
-        // both weights resident in LDS (at most 66 KB at H = 4C)
-        const int limit = fused_lds_limit();
-        if (limit <= 0 || trans_rows_lds_bytes(64, a.H) <= (size_t)limit) return run_transition_rows<ADD, BF>(a, s);
-    }
-    using T = TransTile<C>;
-    constexpr int TH = trans_threads(C);
-    constexpr int kTR = trans_rows<C>();
-    // the weight chunk buffers: static (two) where double-buffered, else one in the dynamic part
-    constexpr size_t wchunk = (size_t)(T::kW1 + T::kW2) * 2;
-    constexpr bool DB = trans_double_buffer(C);
-    const size_t lds = (size_t)kTR * C * 2 + (DB ? 0 : wchunk) + (size_t)(3 * C + a.H) * 4;
-    const size_t total = lds + (DB ? 2 * wchunk : 0);
     const int limit = fused_lds_limit();
-    if (limit > 0 && total > (size_t)limit) {
-        return invalid("transition: needs " + std::to_string(total / 1024) + " KB shared, device allows " +
+    // C = 64: both weights resident in LDS (at most 66 KB at H = 4C); wider: the row tile, one
+    // weight chunk, the LayerNorm parameters and the biases
+    using T = TransTile<C>;
+    constexpr int kTR = trans_rows<C>();
+    const size_t lds = C == 64 ? trans_rows_lds_bytes(64, a.H)
+                               : (size_t)kTR * C * 2 + (size_t)(T::kW1 + T::kW2) * 2 + (size_t)(3 * C + a.H) * 4;
+    if (limit > 0 && lds > (size_t)limit) {
+        return invalid("transition: needs " + std::to_string(lds / 1024) + " KB shared, device allows " +
                        std::to_string(limit / 1024) + " KB");
     }
-    const int64_t tiles = (a.M + kTR - 1) / kTR;
-    const dim3 grid(persistent_grid(tiles, total, trans_per_cu(C)));
-    if (int st = launch_fused("transition", transition_kernel<C, ADD, TH, BF>, grid, lds, s, &a, 0)) return st;
-    stage_mark(s, 0);
-    hipLaunchKernelGGL((transition_kernel<C, ADD, TH, BF>), grid, dim3(TH), lds, s, a);
-    stage_mark(s, 1);
-    return launch_status("transition");
+    if constexpr (C == 64) {
+        return run_transition_rows<ADD, BF>(a, s);
+    } else {
+        constexpr int TH = trans_threads(C);
+        const int64_t tiles = (a.M + kTR - 1) / kTR;
+        const dim3 grid(persistent_grid(tiles, lds, 1));
+        if (int st = launch_fused("transition", transition_kernel<C, ADD, TH, BF>, grid, lds, s, &a, 0)) return st;
+        stage_mark(s, 0);
+        hipLaunchKernelGGL((transition_kernel<C, ADD, TH, BF>), grid, dim3(TH), lds, s, a);
+        stage_mark(s, 1);
+        return launch_status("transition");
+    }
 }
 
 extern "C" int clk_transition(clk_stream stream, const clk_buffer* x, const clk_buffer* scale,
