@@ -1578,6 +1578,8 @@ __global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(T
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) hacc[h2][rb] = mfma16x16x32(w, yf[rb][ks], hacc[h2][rb]);
                 }
+            // (one product's fragment reads in flight at a time: hoisting more costs registers)
+            __builtin_amdgcn_sched_barrier(0);
             // relu(. + b1), fp16: slot 8 g + e of step p is hidden unit 32 p + 8 g + e
             half8 hop[RB];
 #pragma unroll
@@ -1585,6 +1587,7 @@ __global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(T
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     hop[rb][e] = (half_t)fmaxf(hacc[e >> 2][rb][e & 3] + b1l[32 * p + e], 0.f);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
                 const half8 w = fld8(W2 + frag(cb, p, KH, lane));
@@ -1606,10 +1609,12 @@ __global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(T
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float res = ADD ? act_get<BF>(xr[rb][cp], e) : 0.f;
-                    o[e] = act_cvt<BF>(work == kPadding ? 0.f : acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + res);
+                    o[e] = act_cvt<BF>(acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + res);
                 }
+                // a padding tile stores zeros (with add_input it stores nothing)
+                const u32x4 ov = !ADD && work == kPadding ? u32x4{0u, 0u, 0u, 0u} : __builtin_bit_cast(u32x4, o);
                 const uint32_t off = (uint32_t)((16 * rb + r16) * C + col) * 2u;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), ro, store ? off : kDrop, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(ov, ro, store ? off : kDrop, 0, 0);
             }
     };
 
