@@ -77,8 +77,13 @@ def attention(q, k, v, bias, kmask, scale=None, block_q=None, block_k=None):
 def gated_attention(q, k, v, bias, kmask, gate, gate_bias=None, scale=None):
     """attention(...) * sigmoid(gate + gate_bias), differentiable in the gate too.
 
-    gate [N,H,Sq,D]; gate_bias [H,D] or [H*D] (zeros if None). The product is taken in fp32 and
-    rounded to fp16 once, as the gated packed forward does (cuda/volta_attn.h:46-52)."""
+    gate [N,H,Sq,D]; gate_bias [H,D] or [H*D] (zeros if None). The attention output o comes back
+    from the kernel already rounded to fp16; the product o * sigmoid(g) is taken in fp32 and
+    rounded to fp16 again. The result therefore carries two roundings, where the reference's gated
+    packed forward gates the fp32 output and rounds once (cuda/volta_attn.h:46-52): the two
+    differ by at most about one fp16 ulp of the result (|sigmoid| <= 1, so o's rounding error of
+    half an ulp of o is at most half an ulp of the product's scale, plus the product's own half
+    ulp). VoltaMmaPacked with G = 4 (attention_packed) is the single-rounding forward."""
     o = attention(q, k, v, bias, kmask, scale)
     g = gate.float()
     if gate_bias is not None:

@@ -380,6 +380,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
             keep_cur = __ballot(mbyte != 0u);
             stage(buf ^ 1, keep_cur);
         }
+        // at DP = 32 the next tile's K and V, loaded straight into LDS at the start of this tile,
+        // have landed before the barrier after which every wave reads them (the compiler also
+        // waits for all loads before a barrier; the order does not rest on it)
+        if constexpr (DP == 32) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     };
 
@@ -1342,6 +1346,10 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
                 r[128] = make_float4(accv[0][0], accv[0][1], accv[0][2], accv[0][3]);
                 r[192] = make_float4(accv[1][0], accv[1][1], accv[1][2], accv[1][3]);
             }
+            // the next step's tiles and terms, loaded straight into LDS at the start of this
+            // step, have landed before the barrier after which every wave reads them (the
+            // compiler also waits for all loads before a barrier; the order does not rest on it)
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         }
 

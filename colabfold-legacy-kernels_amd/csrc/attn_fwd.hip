@@ -350,7 +350,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     // covers only the loads it needs.
     uint64_t keep_cur = 0u;
     const int k_last = (k_end - 1) / T::kBK * T::kBK;
-    const auto tile = [&](auto vec, int k0, int buf, H16 (&bias16)[T::kQB],
+    const auto tile = [&](auto vec, auto first, int k0, int buf, H16 (&bias16)[T::kQB],
                           H16 (&bias_next)[T::kQB]) __attribute__((always_inline)) {
         const half_t* Ks = DP == 32 ? (buf ? K32b : K32a) : Ks2[buf & (DP == 32 ? 0 : 1)];
         const half_t* Vs = DP == 32 ? (buf ? V32b : V32a) : Vs2[buf & (DP == 32 ? 0 : 1)];
@@ -373,48 +373,54 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         // every key of the tile kept and inside Sk: the bias stands as loaded
         if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
 
-        // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4
+        // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4, fragment-major;
+        // then the natural-domain logits t = scale s + bias: a masked key's s is 0 (its K row
+        // staged as zeros) and its bias the masked logit, a key past Sk has bias -inf
         float4v s[4][T::kQB];
+        const auto logits = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            // key 16 (r/4) + 4 kb + r%4, fragment-major
+            for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-            for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
+                for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < T::kKS; ++ks) {
-                const half8 kop = ld8(&Ks[((kb * T::kKS + ks) * kWave + lane) * 8]);
+                for (int ks = 0; ks < T::kKS; ++ks) {
+                    const half8 kop = ld8(&Ks[((kb * T::kKS + ks) * kWave + lane) * 8]);
 #pragma unroll
-                for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
-            }
-        }
-
-        // natural-domain logits t = scale s + bias: a masked key's s is 0 (its K row staged as
-        // zeros) and its bias the masked logit, a key past Sk has bias -inf
-        float m_tile[T::kQB];
-#pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int kk = 4 * kb + i;
-                    const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
-                    const float t = fmaf(s[kb][qb][i], scale, (float)b);
-                    s[kb][qb][i] = t;
-                    mx = fmaxf(mx, t);
+                    for (int qb = 0; qb < T::kQB; ++qb) s[kb][qb] = mfma16x16x32(kop, qop[qb][ks], s[kb][qb]);
                 }
-            m_tile[qb] = mx;
-        }
+            }
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb)
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = 4 * kb + i;
+                        const half_t b = kk < 8 ? bias16[qb].lo[kk] : bias16[qb].hi[kk - 8];
+                        s[kb][qb][i] = fmaf(s[kb][qb][i], scale, (float)b);
+                    }
+        };
+        logits();
 
         // lazy max: move only when some query of the wave gains more than 6 in log2 units. A
         // query's tile max is the largest of its four lanes' maxima, so the per-lane test decides
-        // the same; the cross-lane maximum is only needed on a tile that raises.
-        bool up = false;
+        // the same; the cross-lane maximum is only needed on a tile that raises. Returns whether
+        // the wave moved (always on the first tile, where thr is -inf).
+        const auto lazy_max = [&]() __attribute__((always_inline)) -> bool {
+            float m_tile[T::kQB];
+            bool up = false;
 #pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) up |= m_tile[qb] * kLog2e > thr[qb];
-        if (__any(up)) {
-            // the running max moves (always on the first tile): rescale l and O by 2^(m - m_new)
+            for (int qb = 0; qb < T::kQB; ++qb) {
+                float mx = s[0][qb][0];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][qb][i]);
+                m_tile[qb] = mx;
+                up |= m_tile[qb] * kLog2e > thr[qb];
+            }
+            if (!__any(up)) return false;
+            // the running max moves: rescale l and O by 2^(m - m_new)
 #pragma unroll
             for (int qb = 0; qb < T::kQB; ++qb) {
                 const float m_new = fmaxf(m_run[qb], wave_xor_max4(m_tile[qb]));
@@ -429,23 +435,50 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
                 nm2[qb] = -m_new * kLog2e;
                 thr[qb] = m_new * kLog2e + 6.f;
             }
-        }
+            return true;
+        };
 
+        // p = 2^(t log2e - m log2e), packed to fp16 for the P.V product, and the tile's fp32 sum
+        // of p per query (of this lane's 16 keys)
         half8 pb[2][T::kQB];
+        float lt[T::kQB];
+        const auto probs = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < T::kQB; ++qb) {
-            float lsum = 0.f;
+            for (int qb = 0; qb < T::kQB; ++qb) {
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
+                for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = exp2_fast(fmaf(s[kb][qb][i], kLog2e, nm2[qb]));
-                    lsum += p;
-                    pb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)p;
+                    for (int i = 0; i < 4; ++i) {
+                        const float p = exp2_fast(fmaf(s[kb][qb][i], kLog2e, nm2[qb]));
+                        lt[qb] = kb == 0 && i == 0 ? p : lt[qb] + p;
+                        pb[kb >> 1][qb][4 * (kb & 1) + i] = (half_t)p;
+                    }
                 }
             }
-            l_run[qb] += lsum;
+        };
+        if constexpr (decltype(first)::value) {
+            lazy_max();
+            probs();
+        } else {
+            // A logit above the running max by more than 6 has p > 2^6; p >= 0, so a lane whose
+            // 16 p of a query sum to at most 64 holds none for that query. Only a wave where some
+            // lane's sum exceeds 64 takes the exact test, on the logits formed again (bias
+            // included) rather than kept live through the tile, and p again if the max moved.
+            probs();
+            bool hot = false;
+#pragma unroll
+            for (int qb = 0; qb < T::kQB; ++qb) hot |= !(lt[qb] <= 64.f);
+            if (__any(hot)) {
+                if constexpr (decltype(vec)::value) {
+                    read_bias(buf, bias16);
+                    if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
+                }
+                logits();
+                if (lazy_max()) probs();
+            }
         }
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) l_run[qb] += lt[qb];
 
         // O^T += V^T P^T: A row r of d block db is d = (DP/4)(r/4) + 4 db + r%4; slot 8 g + j of
         // contraction step kt is key 16 g + 8 kt + j, which is where P^T already sits. V^T is
@@ -465,6 +498,10 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             keep_cur = __ballot(mbyte != 0u);
             stage(buf ^ 1, keep_cur);
         }
+        // at DP = 32 the next tile's K and V, loaded straight into LDS at the start of this tile,
+        // have landed before the barrier after which every wave reads them (the compiler also
+        // waits for all loads before a barrier; the order does not rest on it)
+        if constexpr (DP == 32) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     };
 
@@ -481,9 +518,10 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         keep_cur = __ballot(mbyte != 0u);
         stage(0, keep_cur);
         __syncthreads();
-        for (int k0 = 0; k0 < k_end; k0 += 2 * T::kBK) {
-            tile(vec, k0, 0, biasA, biasB);
-            if (k0 + T::kBK < k_end) tile(vec, k0 + T::kBK, 1, biasB, biasA);
+        tile(vec, std::true_type{}, 0, 0, biasA, biasB);
+        for (int k0 = T::kBK; k0 < k_end; k0 += 2 * T::kBK) {
+            tile(vec, std::false_type{}, k0, 1, biasB, biasA);
+            if (k0 + T::kBK < k_end) tile(vec, std::false_type{}, k0 + T::kBK, 0, biasA, biasB);
         }
         // the last tile's bias loads (of itself, unused) land before the workgroup's LDS is freed
         if constexpr (decltype(vec)::value) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -97,7 +97,9 @@ size_t clk_attention_bwd_workspace_size(int32_t device, const clk_buffer* q, con
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same buffers, flags,
  * validation and results (bit-identical), but no workspace argument: the scratch is a static
  * device array of the library, one per GPU, of clk_attention_bwd_noalloc_scratch_size() bytes
- * (96 MiB, enough for [512, 8, 384, 32]), held until the process ends. Shapes whose scratch
+ * (96 MiB, enough for [512, 8, 384, 32]), held until the process ends. The array is part of the
+ * library's code object, so loading the library reserves those 96 MiB on every GPU it runs a
+ * kernel on, whether or not this entry point is ever called. Shapes whose scratch
  * would exceed it are rejected with CLK_INVALID_ARGUMENT before any launch. The call allocates
  * nothing. Every call on a GPU shares that GPU's scratch, so calls that overlap on one GPU (two
  * streams, or two threads) race and must be serialised by the caller. */

@@ -151,27 +151,45 @@ def test_transition_bf16(hip, c, factor, m, s, mean, add):
     check(npy(out), want, "transition")
 
 
-def test_keep_bf16(hip):
+@pytest.mark.parametrize("c", (64, 128))
+def test_keep_bf16(hip, c):
     """keep with bf16 activations: real rows identical with and without keep, rows of padded
-    tiles zero or (where the output aliases x) unchanged (tests/test_keep.py)."""
-    S, n, c = 192, 65, 128
+    tiles zero or (where the output aliases x) unchanged (tests/test_keep.py); the transition at
+    4C (and 2C at c = 64) and the tri-mul epilogue."""
+    S, n = 192, 65
     live = ((np.arange(S) < n)[:, None] & (np.arange(S) < n)[None, :]).reshape(-1)
-    rng = rng_for("keep bf16")
+    rng = rng_for("keep bf16", c)
     m = live.size
     x, tx = bf(rng, m, c, s=2.)
     tkeep = cu(live.astype(np.float16))[0]
     sc, of = f32(rng, c, s=.1, mean=1.), f32(rng, c, s=.1)
-    tw = cu(sc, of, np.ascontiguousarray(f16(rng, c, 4 * c, s=c ** -.5).T), f16(rng, 4 * c, s=.1),
-            orf.w2_blocked(f16(rng, 4 * c, c, s=(4 * c) ** -.5)), f16(rng, c, s=.1))
-    for add in (False, True):
-        a0, a1 = tx.clone(), tx.clone()
-        plain = npy(hip.transition(a0, *tw, eps=EPS, add_input=add, out=a0 if add else None))
-        kept = npy(hip.transition(a1, *tw, keep=tkeep, eps=EPS, add_input=add,
-                                  out=a1 if add else None))
-        assert np.array_equal(kept[live], plain[live]), "real rows differ (add=%s)" % add
+
+    def check_rows(kept, plain, pad, label):
+        assert np.array_equal(kept[live], plain[live]), "real rows differ (%s)" % label
         # padding is decided per row tile: a padded row is the plain result (its tile holds a
         # live row) or the padding value (x where the output aliases it, else zero)
-        pad = x[~live] if add else 0.0
         ok = (kept[~live] == plain[~live]) | (kept[~live] == pad)
-        assert ok.all(), "padded rows (add=%s)" % add
-        assert (kept[~live] == pad).any(), "no row was padded (add=%s)" % add
+        assert ok.all(), "padded rows (%s)" % label
+        assert (kept[~live] == pad).any(), "no row was padded (%s)" % label
+
+    for factor in ((2, 4) if c == 64 else (4,)):
+        hd = factor * c
+        tw = cu(sc, of, np.ascontiguousarray(f16(rng, c, hd, s=c ** -.5).T), f16(rng, hd, s=.1),
+                orf.w2_blocked(f16(rng, hd, c, s=hd ** -.5)), f16(rng, c, s=.1))
+        for add in (False, True):
+            a0, a1 = tx.clone(), tx.clone()
+            plain = npy(hip.transition(a0, *tw, eps=EPS, add_input=add, out=a0 if add else None))
+            kept = npy(hip.transition(a1, *tw, keep=tkeep, eps=EPS, add_input=add,
+                                      out=a1 if add else None))
+            check_rows(kept, plain, x[~live] if add else 0.0,
+                       "transition c=%d x%d add=%s" % (c, factor, add))
+    x_cm = f32(rng, c, m, s=20.)
+    g = cu(x_cm, sc, of, f32(rng, c, s=.1, mean=1.), f32(rng, c, s=.1), f16(rng, c, c, s=.1),
+           f16(rng, c, s=.1), f16(rng, c, c, s=.1), f16(rng, c, s=.1))
+    for add in (False, True):
+        a0, a1 = tx.clone(), tx.clone()
+        plain = npy(hip.trimul_epilogue(g[0], a0, *g[1:], eps=EPS, add_input=add,
+                                        out=a0 if add else None))
+        kept = npy(hip.trimul_epilogue(g[0], a1, *g[1:], keep=tkeep, eps=EPS, add_input=add,
+                                       out=a1 if add else None))
+        check_rows(kept, plain, x[~live] if add else 0.0, "epilogue c=%d add=%s" % (c, add))

@@ -169,28 +169,34 @@ def check_keep(got_keep, got_plain, keep_rows, pad_value, label, rows_axis=0):
     assert pad_ok.all(), label + ": a padded row is neither the plain result nor the padding value"
 
 
+@pytest.mark.parametrize("c", (64, 128))
 @pytest.mark.parametrize("label,live", KEEP_CASES, ids=[c[0] for c in KEEP_CASES])
-def test_keep(hip, label, live):
-    rng = rng_for("keep", label)
-    m, c, n, h = live.size, 128, 128, 4
+def test_keep(hip, label, live, c):
+    """At c = 64 the transition (2C and 4C) runs the resident-weight kernel, whose keep decision
+    is a ballot per 64-row unit, and the epilogue its C = 64 tiles; at c = 128 the chunked
+    transition and the 128-channel epilogue."""
+    rng = rng_for("keep", label, c)
+    m, n, h = live.size, 128, 4
     keep = live.astype(np.float16)
     tkeep = cu(keep)[0]
     x = f16(rng, m, c, s=2.)
     sc, of = f32(rng, c, s=.1, mean=1.), f32(rng, c, s=.1)
     tx, tsc, tof = cu(x, sc, of)
     # transition, with and without add_input
-    w1T, b1 = f16(rng, 4 * c, c, s=c ** -.5), f16(rng, 4 * c, s=.1)
-    w2T, b2 = orf.w2_blocked(f16(rng, 4 * c, c, s=(4 * c) ** -.5)), f16(rng, c, s=.1)
-    tw = cu(w1T, b1, w2T, b2)
-    for add in (False, True):
-        plain_in = tx.clone()
-        plain = npy(hip.transition(plain_in, tsc, tof, *tw, eps=EPS, add_input=add,
-                                   out=plain_in if add else None))
-        kin = tx.clone()
-        kept = npy(hip.transition(kin, tsc, tof, *tw, keep=tkeep, eps=EPS, add_input=add,
-                                  out=kin if add else None))
-        check_keep(kept, plain, live, x.astype(np.float32) if add else 0.0,
-                   "%s transition add=%s" % (label, add))
+    for factor in ((2, 4) if c == 64 else (4,)):
+        hd = factor * c
+        w1T, b1 = f16(rng, hd, c, s=c ** -.5), f16(rng, hd, s=.1)
+        w2T, b2 = orf.w2_blocked(f16(rng, hd, c, s=hd ** -.5)), f16(rng, c, s=.1)
+        tw = cu(w1T, b1, w2T, b2)
+        for add in (False, True):
+            plain_in = tx.clone()
+            plain = npy(hip.transition(plain_in, tsc, tof, *tw, eps=EPS, add_input=add,
+                                       out=plain_in if add else None))
+            kin = tx.clone()
+            kept = npy(hip.transition(kin, tsc, tof, *tw, keep=tkeep, eps=EPS, add_input=add,
+                                      out=kin if add else None))
+            check_keep(kept, plain, live, x.astype(np.float32) if add else 0.0,
+                       "%s transition c=%d x%d add=%s" % (label, c, factor, add))
     # ln_projection
     wT, wbT = f16(rng, 4 * n, c, s=.1), f16(rng, h, c, s=.1)
     twT, twb = cu(wT, wbT)
