@@ -174,9 +174,10 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
 
     // K/V chunks of the next key tile, one tile ahead of their LDS store: fixed row and column
     // per lane, buffer loads whose range is the tile's rows below Sk (a row past Sk and a column
-    // past D read zeros). Lane l of every wave also loads the mask byte of key k0 + l (zero past
-    // Sk); a wave ballot of those bytes is the tile's keep bits. A masked key's K row is staged
-    // as zeros.
+    // past D read zeros). The mask bytes run a tile further ahead: lane l of every wave loads the
+    // byte of key k0 + l (zero past Sk) of the tile after the next, so a wave ballot of them (the
+    // tile's keep bits, uniform across the workgroup) is known, with no wait, when that tile's K/V
+    // loads are issued. A masked key's K row is staged as zeros.
     uint32_t kvoff[T::kCPT];
     int krow[T::kCPT], kdst[T::kCPT];
 #pragma unroll
@@ -191,7 +192,11 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
     const char* const vb_base = reinterpret_cast<const char*>(a.v + kbase);
     const char* const mrow = reinterpret_cast<const char*>(a.kmask + (int64_t)n * a.Sk);
     half8 kreg[T::kCPT], vreg[T::kCPT];
-    uint32_t mbyte = 0u;
+    const auto fetch_mask = [&](int k0) -> uint32_t {
+        const int rows = min(a.Sk - k0, T::kBK);
+        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
+        return __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
+    };
     const auto fetch = [&](int k0) {
         const int rows = min(a.Sk - k0, T::kBK);
         const int64_t kofs = (int64_t)k0 * a.D * 2;
@@ -202,16 +207,15 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
             kreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rk, kvoff[i], 0, 0));
             vreg[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, kvoff[i], 0, 0));
         }
-        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
-        mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
     // At DP = 32 the K and V tiles go from memory straight into LDS by direct-to-LDS loads
     // (buffer_load ... lds), one 1 KB load of each per wave, issued at the start of the previous
     // tile and complete at its closing barrier. Their rows are unpadded 64 bytes with the 16-byte
     // chunks of LDS row R at chunk position c ^ ((R / 4) % 4), so the row-form reads of 16
     // consecutive rows fall on 16 distinct bank groups: slot l of wave w's load is LDS row
-    // R = 16 w + l / 4 (key x with perm_row(x, 16) = R), position l % 4. Masked keys' K rows are
-    // zeroed in LDS once the loads have landed.
+    // R = 16 w + l / 4 (key x with perm_row(x, 16) = R), position l % 4. A masked key's K slots
+    // take an offset past the buffer's range, so the load itself writes their zeros; the first
+    // tile, loaded before its keep bits are known, is zeroed in LDS instead.
     uint32_t kvdma = 0u;
     int dkey = 0;
     if constexpr (DP == 32) {
@@ -220,26 +224,27 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
         const int col = 8 * (pos ^ ((R >> 2) & 3));
         kvdma = col < a.D ? (uint32_t)((dkey * a.D + col) * 2) : 0x80000000u;
     }
-    const auto dma_kv = [&](int k0, int buf) {
+    const auto dma_kv = [&](int k0, int buf, uint64_t keep) {
         const int rows = min(a.Sk - k0, T::kBK);
         const int64_t kofs = (int64_t)k0 * a.D * 2;
         const int range = __builtin_amdgcn_readfirstlane(rows * a.D * 2);
         const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb_base + kofs), 0, range, 0x00020000);
         const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb_base + kofs), 0, range, 0x00020000);
+        const uint32_t koff = (keep >> dkey) & 1u ? kvdma : 0x80000000u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rk, (__attribute__((address_space(3))) void*)((buf ? K32b : K32a) + 512 * wv), 16, kvdma, 0, 0, 0);
+            rk, (__attribute__((address_space(3))) void*)((buf ? K32b : K32a) + 512 * wv), 16, koff, 0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rv, (__attribute__((address_space(3))) void*)((buf ? V32b : V32a) + 512 * wv), 16, kvdma, 0, 0, 0);
-        const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
-        mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
-    const auto fetch_kv = [&](int k0, int buf) {
+    const auto fetch_kv = [&](int k0, int buf, uint64_t keep) {
         if constexpr (DP == 32) {
-            dma_kv(k0, buf);
+            dma_kv(k0, buf, keep);
         } else {
             fetch(k0);
         }
     };
+    // the register-staged tile into LDS buffer buf, masked K rows as zeros (DP != 32); at DP = 32
+    // the zeroing of the first tile's masked K rows, once its loads have landed
     const auto stage = [&](int buf, uint64_t keep) {
         if constexpr (DP == 32) {
             if (keep != ~0ull) {
@@ -301,15 +306,22 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
     // dP^T starts from -delta (the MFMA accumulator input), so dS = p dP is one multiply
     float4v ndlt[T::kQB];
 
+    // keep bits of this tile, and the mask byte of the next tile (loaded a tile ago)
     uint64_t keep_cur = 0u;
+    uint32_t mbyte = 0u;
+    const int k_last = a.Sk > 0 ? (a.Sk - 1) / T::kBK * T::kBK : 0;
     const auto tile = [&](int k0, int buf, BH16 (&bias16)[T::kQB], BH16 (&bias_next)[T::kQB]) {
         const half_t* Ks = DP == 32 ? (buf ? K32b : K32a) : Ks2[buf & (DP == 32 ? 0 : 1)];
         const half_t* Vs = DP == 32 ? (buf ? V32b : V32a) : Vs2[buf & (DP == 32 ? 0 : 1)];
-        const bool more = k0 + T::kBK < a.Sk;
-        if (more) {
-            fetch_kv(k0 + T::kBK, buf ^ 1);
-            fetch_bias(k0 + T::kBK, bias_next);
-        }
+        // the next tile's K, V and bias and the mask byte of the one after it, issued
+        // unconditionally (past the last tile the last one again, unused): with no branch
+        // around the loads the compiler knows how many are in flight, and no value they bring is
+        // examined before the barrier that ends the tile, so they stay in flight until then
+        const uint64_t keep_next = __ballot(mbyte != 0u);
+        const int kn = min(k0 + T::kBK, k_last);
+        fetch_kv(kn, buf ^ 1, keep_next);
+        fetch_bias(kn, bias_next);
+        mbyte = fetch_mask(min(k0 + 2 * T::kBK, k_last));
         // every key of the tile kept and inside Sk: the bias stands as loaded
         if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
 
@@ -375,29 +387,37 @@ __global__ __launch_bounds__(DqTile<DP>::kThreads, DP == 32 ? 4 : 1) void attn_b
                 for (int qb = 0; qb < T::kQB; ++qb) acc[db][qb] = mfma16x16x32(kto, dsb[qb], acc[db][qb]);
             }
         }
-        // the other buffer was last read a tile ago, before the barrier that ended that tile
-        if (more) {
-            keep_cur = __ballot(mbyte != 0u);
-            stage(buf ^ 1, keep_cur);
-        }
-        // at DP = 32 the next tile's K and V, loaded straight into LDS at the start of this tile,
-        // have landed before the barrier after which every wave reads them (the compiler also
-        // waits for all loads before a barrier; the order does not rest on it)
-        if constexpr (DP == 32) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // (DP != 32) the next tile's registers into the other buffer, last read a tile ago,
+        // before the barrier that ended that tile
+        if constexpr (DP != 32) stage(buf ^ 1, keep_next);
+        // every load of this tile has landed before the barrier after which the waves read the
+        // next tile's K and V (the compiler also waits for all loads before a barrier; the order
+        // does not rest on it), by a waitcnt the compiler sees, so it knows that nothing is in
+        // flight past the barrier
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
         __syncthreads();
+        keep_cur = keep_next;
     };
 
     BH16 biasA[T::kQB], biasB[T::kQB];
+    uint32_t mbyte0 = 0u;
     if (a.Sk > 0) {
-        fetch_kv(0, 0);
+        // the first tile's K and V before its keep bits are known (its masked K rows are zeroed
+        // in LDS below), its bias, and the mask bytes of the first two tiles
+        mbyte0 = fetch_mask(0);
+        fetch_kv(0, 0, ~0ull);
         fetch_bias(0, biasA);
+        mbyte = fetch_mask(min(T::kBK, k_last));
     }
     load_queries();
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) ndlt[qb] = float4v{-dlt[qb], -dlt[qb], -dlt[qb], -dlt[qb]};
     if (a.Sk > 0) {
-        keep_cur = __ballot(mbyte != 0u);
+        keep_cur = __ballot(mbyte0 != 0u);
         stage(0, keep_cur);
+        // the prologue's loads (the first tile, Q, dO, O, lse) have all landed before the loop,
+        // and the compiler knows it: the loop's waits then count only the loop's own loads
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
         __syncthreads();
     }
     for (int k0 = 0; k0 < a.Sk; k0 += 2 * T::kBK) {

@@ -37,6 +37,12 @@ __device__ __forceinline__ float4v mfma16x16x32(half8 a, half8 b, float4v c) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8), for __builtin_amdgcn_s_waitcnt: unlike an asm statement, the
+// compiler's own wait insertion sees it and knows that no vector memory access is in flight after
+// it.
+constexpr int kWaitVm0 = 0x0F70;
+
 // Activations of the fused ops are fp16 (the reference's F16 contract) or bf16 (BF). Loads keep
 // the raw 16-bit patterns in half8 registers and convert where the value is used; a bf16 value
 // converts to fp16 exactly within fp16's normal range, so MFMA operands stay fp16. Results are
