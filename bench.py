@@ -456,6 +456,37 @@ def bench_fused(torch, hip, iters, warmup):
     return res
 
 
+def hbm_ceiling(torch, iters=20, gib=1):
+    """The attainable HBM bandwidth of plain streaming kernels on this box, for reading the fused
+    ops' fractions: torch's copy (read + write), fill (write only) and row sums of an fp32 view (read
+    only; the fastest torch reduction measured, within 2% of a hand-written 16-byte read loop) of
+    `gib` GiB buffers, far past the 256 MB MALL; GB/s of the mean over `iters` calls (bytes moved
+    by the kernel / time)."""
+    n = gib << 30
+    src = torch.ones(n // 2, dtype=torch.int16, device="cuda")
+    dst = torch.empty_like(src)
+    red = src.view(torch.float32).view(65536, -1)
+    out = {}
+    for name, fn, byts in (("copy", lambda: dst.copy_(src), 2 * n),
+                           ("write", lambda: dst.fill_(3), n),
+                           ("read", lambda: red.sum(1), n)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / iters
+        out[name] = {"gbs": round(byts / ms / 1e6, 1), "frac": round(byts / ms / 1e6 / PEAK_GBS, 4),
+                     "ms": round(ms, 4), "bytes": byts}
+    del src, dst, red
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(torch):
     """The fp32 torch-CPU attention fwd+bwd on a row sample of C3, as TFLOP/s."""
     from oracle import cpu_ref
@@ -675,6 +706,7 @@ def main():
         line["packed_fwd"] = bench_packed(torch, hip, args.steps, args.warmup, ev)
     if not args.no_fused:
         line["fused"] = bench_fused(torch, hip, args.steps, args.warmup)
+        line["hbm_ceiling"] = hbm_ceiling(torch)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(line), flush=True)

@@ -1307,48 +1307,44 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
             dma_s(pass + (st + 1) / kSteps, (st + 1) % kSteps, par ^ 1);
             const half_t* buf = (par ? lds1 : lds0) + q3 * 2 * kSub;
             const float* qtb = par ? qterms1 : qterms0;
-            float x[2][8];
-            float4v dp[2][2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            // The step's two tiles as a pipeline: tile 1's S and dP products run beside tile 0's
+            // softmax, and tile 0's dV / dK products beside tile 1's, so that each wave has
+            // matrix-core work in flight while it issues vector instructions.
+            float4v sacc[2][2], dp[2][2];
+            half8 bb[2], pb[2], dsb[2];
+            // S and dP of tile i: the LDS reads and four MFMAs
+            const auto sdp = [&](int i) __attribute__((always_inline)) {
                 const int u = 2 * st + i;
                 const half_t* Qs = buf + i * kSub;
                 const half_t* Os = Qs + kOs;
                 const int qo = 64 * i;
-                const half8 bb = *reinterpret_cast<const half8*>(brow + 32 * u);
+                bb[i] = *reinterpret_cast<const half8*>(brow + 32 * u);
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb) {
-                    float4v sacc = *reinterpret_cast<const float4v*>(qtb + qtS + qo + 4 * qb);
+                    sacc[i][qb] = *reinterpret_cast<const float4v*>(qtb + qtS + qo + 4 * qb);
                     dp[i][qb] = *reinterpret_cast<const float4v*>(qtb + qtD + qo + 4 * qb);
                     const int w = 2 * reg_word(16 * qb + r16, 8 * g);
                     const half8 qa = *reinterpret_cast<const half8*>(Qs + w);
                     const half8 oa = *reinterpret_cast<const half8*>(Os + w);
-                    sacc = mfma16x16x32(qa, kop, sacc);
+                    sacc[i][qb] = mfma16x16x32(qa, kop, sacc[i][qb]);
                     dp[i][qb] = mfma16x16x32(oa, vop, dp[i][qb]);
-#pragma unroll
-                    for (int i4 = 0; i4 < 4; ++i4)
-                        x[i][4 * qb + i4] = fmaf(sacc[i4], c1s, (float)bb[4 * qb + i4]) * kLog2e;
                 }
-            }
-            half8 pb[2], dsb[2];
-            float dsf[2][8];
+            };
+            // the softmax of tile i: s2 = log2e (scale S + bias), p, dS = p dP, their fp16
+            // operands and the dBias adds
+            const auto soft = [&](int i) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const float p = exp2_fast(x[i][j]);
-                    dsf[i][j] = pin_f32(p * dp[i][j >> 2][j & 3]);
+                for (int j = 0; j < 8; ++j) {
+                    const float x = fmaf(sacc[i][j >> 2][j & 3], c1s, (float)bb[i][j]) * kLog2e;
+                    const float p = exp2_fast(x);
+                    const float dsf = pin_f32(p * dp[i][j >> 2][j & 3]);
                     pb[i][j] = (half_t)p;
-                    dsb[i][j] = (half_t)dsf[i][j];
+                    dsb[i][j] = (half_t)dsf;
+                    if constexpr (DBIAS) dbias[2 * st + i][j] = pin_f32(dbias[2 * st + i][j] + dsf);
                 }
-            if constexpr (DBIAS) {
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) dbias[2 * st + i][j] = pin_f32(dbias[2 * st + i][j] + dsf[i][j]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            };
+            // dV^T += dO^T P and dK^T += Q^T dS of tile i (k-slots queries 8 g + j, read transposed)
+            const auto dvdk = [&](int i) __attribute__((always_inline)) {
                 const half_t* Qs = buf + i * kSub;
                 const half_t* Os = Qs + kOs;
 #pragma unroll
@@ -1358,7 +1354,34 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
                     accv[db] = mfma16x16x32(ot, pb[i], accv[db]);
                     acck[db] = mfma16x16x32(qt, dsb[i], acck[db]);
                 }
+            };
+            sdp(0);
+            sdp(1);
+            soft(0);
+            dvdk(0);
+            soft(1);
+            dvdk(1);
+#ifdef CLK_REG3_SGB
+            // tile 0's reads and products; tile 1's reads; tile 1's products each beside a quarter
+            // of tile 0's softmax; tile 0's transposed reads; its dV / dK products each beside a
+            // quarter of tile 1's softmax; tile 1's transposed reads and products
+            __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+#endif
             if (st == kSteps - 1 && q3 > 0) {
                 float4* r = red + ((q3 - 1) * 4 + kg) * 4 * 64 + lane;
                 r[0] = make_float4(acck[0][0], acck[0][1], acck[0][2], acck[0][3]);
