@@ -279,15 +279,15 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     // measured a sixth of the kernel's time. Instead the wave loads its 32 x 64 bias tile with
     // four direct-to-LDS loads (buffer_load ... lds) from a buffer whose range is the head's bias
     // block, each a contiguous sweep of 8 rows x 128 bytes: lane 8 r + j of load m reads row 8 m + r,
-    // 16-byte segment (j - 2 (r / 2)) % 8, and lands at byte 1040 m + 16 (8 r + j) of the wave's
-    // buffer. The rotation and the 16-byte skew between loads put the 16 rows of each 16-lane read
-    // on distinct LDS banks. Rows past Sq lie past the buffer's range and read zeros (their
+    // 16-byte segment j ^ 2 (r / 2), and lands at byte 1040 m + 16 (8 r + j) of the wave's buffer,
+    // so key k of row 8 m + r sits at byte 1040 m + 128 r + (2 k ^ 32 (r / 2)). The swizzle and the
+    // 16-byte skew between loads put the 16 rows of each 16-lane read on distinct LDS banks. Rows past Sq lie past the buffer's range and read zeros (their
     // results are never stored); keys past Sk read the next row's values or zeros and become -inf
     // when their tile comes up.
     const half_t* const bias_head = a.bias + (int64_t)h * a.Sq * a.Sk;
     uint32_t bdma[4];
     {
-        const int r = lane >> 3, seg = ((lane & 7) - 2 * (r >> 1)) & 7;
+        const int r = lane >> 3, seg = (lane & 7) ^ (2 * (r >> 1));
         bdma[0] = (uint32_t)(q0w + r) * (uint32_t)a.Sk * 2u + 16u * (uint32_t)seg;
 #pragma unroll
         for (int m = 1; m < 4; ++m) bdma[m] = bdma[0] + (uint32_t)m * 16u * (uint32_t)a.Sk;
@@ -306,11 +306,35 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
 #pragma unroll
         for (int qb = 0; qb < T::kQB; ++qb) {
             const int m = 2 * qb + (r16 >> 3), r = r16 & 7;
-            const half_t* p = &Bs[wv][bb][520 * m + 8 * (8 * r + ((2 * g + 2 * (r >> 1)) & 7))];
+            const half_t* p = &Bs[wv][bb][520 * m + 8 * (8 * r + ((2 * g) ^ (2 * (r >> 1))))];
             b[qb].lo = ld8(p);
             b[qb].hi = ld8(p + 8);
         }
     };
+    // Dead keys of a tile whose bias came through LDS, when they are few: each takes its logit in
+    // the wave's own bias tile before the tile's reads, one LDS store per key from the wave's
+    // first 32 lanes (one query row each) in a scalar loop over the keys (the keep ballot is
+    // uniform): the masked logit inside Sk, -inf past it. Tiles with more dead keys fix the bias
+    // registers instead (fix_bias, a fixed cost per tile).
+    typedef __attribute__((address_space(3))) char lds_char;
+    lds_char* const kill_row = (lds_char*)(&Bs[wv][0][0]) + 1040 * ((lane & 31) >> 3) + 128 * (lane & 7);
+    const uint32_t kill_x = 32u * (uint32_t)((lane & 7) >> 1);
+    const auto kill_bias_lds = [&](int bb, int k0, uint64_t keep64) {
+        if (lane >= 32) return;
+        const int kvalid = a.Sk - k0;
+        const uint64_t inside = kvalid >= 64 ? ~0ull : (1ull << kvalid) - 1ull;
+        lds_char* const row = kill_row + bb * (int)sizeof(Bs[0][0]);
+        const auto put = [&](uint64_t keys, half_t v) {
+            while (keys) {
+                const uint32_t k = (uint32_t)__builtin_ctzll(keys);
+                keys &= keys - 1ull;
+                *reinterpret_cast<__attribute__((address_space(3))) half_t*>(row + ((2u * k) ^ kill_x)) = v;
+            }
+        };
+        put(~keep64 & inside, (half_t)kMaskedLogit);
+        put(~keep64 & ~inside, (half_t)(-INFINITY));
+    };
+    constexpr int kKillMax = 8;  // most dead keys per tile that go through LDS stores
     const auto fetch_bias = [&](int k0, H16 (&b)[T::kQB]) {
         if (a.bias_vec && k0 + T::kBK <= a.Sk) {
 #pragma unroll
@@ -355,10 +379,14 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         const half_t* Ks = DP == 32 ? (buf ? K32b : K32a) : Ks2[buf & (DP == 32 ? 0 : 1)];
         const half_t* Vs = DP == 32 ? (buf ? V32b : V32a) : Vs2[buf & (DP == 32 ? 0 : 1)];
         bool more = true;
+        bool reg_fix = keep_cur != ~0ull;
         if constexpr (decltype(vec)::value) {
             // this tile's bias loads, issued a tile ago, are the only loads in flight: wait for
             // them (the compiler does not order LDS reads after direct-to-LDS loads by itself)
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            // (keys past Sk read as dead: their mask bytes load as zero)
+            reg_fix = keep_cur != ~0ull && __builtin_popcountll(~keep_cur) > kKillMax;
+            if (keep_cur != ~0ull && !reg_fix) kill_bias_lds(buf, k0, keep_cur);
             read_bias(buf, bias16);
             const int kn = min(k0 + T::kBK, k_last);
             fetch_kv(kn, buf ^ 1);
@@ -370,8 +398,9 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
                 fetch_bias(k0 + T::kBK, bias_next);
             }
         }
-        // every key of the tile kept and inside Sk: the bias stands as loaded
-        if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
+        // every key of the tile kept and inside Sk: the bias stands as loaded (through LDS a few
+        // dead keys' logits are in place already)
+        if (reg_fix) fix_bias(k0, bias16, keep_cur);
 
         // S^T = K Q^T: A row r of key block kb is key 16 (r/4) + 4 kb + r%4, fragment-major;
         // then the natural-domain logits t = scale s + bias: a masked key's s is 0 (its K row
@@ -471,7 +500,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             if (__any(hot)) {
                 if constexpr (decltype(vec)::value) {
                     read_bias(buf, bias16);
-                    if (keep_cur != ~0ull) fix_bias(k0, bias16, keep_cur);
+                    if (reg_fix) fix_bias(k0, bias16, keep_cur);
                 }
                 logits();
                 if (lazy_max()) probs();

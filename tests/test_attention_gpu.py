@@ -93,6 +93,17 @@ def test_base_shapes(hip, kw):
     check(got, ref, str(kw))
 
 
+@pytest.mark.parametrize("sk,frac", [(184, 0.0), (120, 0.03), (248, 0.05), (256, 0.2)])
+def test_sparse_dead_keys(hip, sk, frac):
+    """Key tiles with a few dead keys, masked inside Sk or past it (Sk % 64 = 56 leaves 8), and
+    with more than the forward's LDS-store limit of 8 (a 20% mask): both ways a tile's dead
+    keys take their logits."""
+    rng = np.random.default_rng(sk)
+    km = (rng.random((3, sk)) >= frac).astype(np.uint8)
+    got, ref = run(hip, sq=96, sk=sk, kmask=km)
+    check(got, ref, "sk=%d frac=%.2f" % (sk, frac))
+
+
 def test_all_masked_row(hip):
     """A batch element with every key masked: a uniform softmax, finite lse, zero dS."""
     km = np.ones((3, 96), np.uint8)
