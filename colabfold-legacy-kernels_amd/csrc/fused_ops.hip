@@ -939,17 +939,19 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
             xt.v[j] = fld8(a.x + (int64_t)m * K + 8 * (part + TPR * j));
     };
     // the reference's keep rule for the tile (rows past M count as 0) and the rows' max(mask, 0)
-    float mv[16];
+    // (0 for NaN), on the fp16 pairs: an 8-row chunk is wholly inside M or past it; a row is live
+    // if its max(mask, 0) is above 0, and the tile holds a zero if some mask has no magnitude bits
+    typedef unsigned short ushort8 __attribute__((ext_vector_type(8)));
+    half8 mvlo, mvhi;
     const auto decide = [&](int t) {
         const int r0 = t * kTileRows + 16 * g;
-        bool live = false, zero = false;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float k = r0 + e < a.M ? (float)(e < 8 ? mlo[e] : mhi[e - 8]) : 0.f;
-            live |= k > 0.f;
-            zero |= k == 0.f;
-            mv[e] = fmaxf(k, 0.f);
-        }
+        const half8 klo = r0 < a.M ? mlo : fzero8(), khi = r0 + 8 < a.M ? mhi : fzero8();
+        mvlo = __builtin_elementwise_max(klo, fzero8());
+        mvhi = __builtin_elementwise_max(khi, fzero8());
+        const bool live = __builtin_reduce_max(__builtin_elementwise_max(mvlo, mvhi)) > (half_t)0.f;
+        const ushort8 mag = __builtin_elementwise_min(__builtin_bit_cast(ushort8, klo) & (unsigned short)0x7fff,
+                                                      __builtin_bit_cast(ushort8, khi) & (unsigned short)0x7fff);
+        const bool zero = __builtin_reduce_min(mag) == 0;
         const bool any_live = __any(live), any_zero = __any(zero);
         return any_live ? (int)kCompute : any_zero ? (int)kPadding : (int)kSkip;
     };
@@ -966,11 +968,12 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
 #pragma unroll
         for (int j = 0; j < CBW; ++j) {
             const int cb = wave + j * TW;
+            // the products start from the biases
             float4v ap[4], ag[4];
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) {
-                ap[rb] = float4v{0.f, 0.f, 0.f, 0.f};
-                ag[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                ap[rb] = float4v{bpv[j], bpv[j], bpv[j], bpv[j]};
+                ag[rb] = float4v{bgv[j], bgv[j], bgv[j], bgv[j]};
             }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -988,10 +991,14 @@ __global__ __launch_bounds__(TH) void ln_gdp_fast_kernel(LnGdpArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int e = 4 * rb + i;
-                    float v = mv[e] * (ap[rb][i] + bpv[j]) * sigmoid_fast(ag[rb][i] + bgv[j]);
-                    v = zero_out ? 0.f : v;
+                    const float mv = (float)(e < 8 ? mvlo[e] : mvhi[e - 8]);
+                    const float v = mv * ap[rb][i] * sigmoid_fast(ag[rb][i]);
                     if (e < 8) lo[e] = act_cvt<BF>(v); else hi[e - 8] = act_cvt<BF>(v);
                 }
+            if (zero_out) {
+                lo = fzero8();
+                hi = fzero8();
+            }
             // column block cb lies wholly in left (columns < PH) or in right
             const int col = 16 * cb + r16;
             const bool is_left = 16 * cb < PH;
