@@ -591,9 +591,37 @@ def traffic_summary(fetch_dir, write_dir, mib, prefix=""):
     return "\n".join(lines)
 
 
+# MI355X: 32 shader engines (8 XCDs x 4) report SQ_BUSY_CYCLES; 256 CUs x 4 SIMDs issue
+SQ_ENGINES, SIMDS = 32, 1024
+
+
+def derived_counters(c):
+    """Utilisation ratios from one kernel's counter means (those whose counters are present):
+    valu, mfma and coexec are shares of the SIMD cycles of the dispatch (SQ_BUSY_CYCLES per shader
+    engine x SIMDs; SQ_ACTIVE_INST_VALU counts quad-cycles) with VALU, MFMA, or both at once busy;
+    lds_conflict the share of LDS-active cycles lost to bank conflicts; wait_lds the share of wave
+    cycles spent waiting on LDS; trans_per_valu transcendental VALU instructions per VALU one."""
+    out = []
+    busy = c.get("SQ_BUSY_CYCLES")
+    if busy:
+        simd = busy / SQ_ENGINES * SIMDS
+        for name, key, k in (("valu", "SQ_ACTIVE_INST_VALU", 4.0), ("mfma", "SQ_VALU_MFMA_BUSY_CYCLES", 1.0),
+                             ("coexec", "SQ_VALU_MFMA_COEXEC_CYCLES", 1.0)):
+            if key in c:
+                out.append("%s=%.3f" % (name, c[key] * k / simd))
+    if c.get("SQ_LDS_IDX_ACTIVE"):
+        out.append("lds_conflict=%.3f" % (c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_LDS_IDX_ACTIVE"]))
+    if c.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_LDS" in c:
+        out.append("wait_lds=%.3f" % (c["SQ_WAIT_INST_LDS"] / c["SQ_WAVE_CYCLES"]))
+    if c.get("SQ_INSTS_VALU") and "SQ_INSTS_VALU_TRANS_F32" in c:
+        out.append("trans_per_valu=%.3f" % (c["SQ_INSTS_VALU_TRANS_F32"] / c["SQ_INSTS_VALU"]))
+    return " ".join(out)
+
+
 def counter_summary(dirs):
     """Mean per dispatch of every counter in one or more rocprofv3 --pmc runs, for each of the
-    library's kernels (one line per kernel, counters in the order first seen)."""
+    library's kernels (one line per kernel, counters in the order first seen), then the kernel's
+    derived ratios (derived_counters) on a line of their own."""
     per, names = {}, []
     for d in dirs:
         files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
@@ -614,8 +642,11 @@ def counter_summary(dirs):
     lines = []
     for name in sorted(acc):
         short = name.replace("void ", "").replace("clk::", "").split("(")[0].replace(" ", "")
-        vals = " ".join("%s=%.4g" % (c, statistics.mean(acc[name][c])) for c in names if c in acc[name])
-        lines.append("%s %s" % (short, vals))
+        means = {c: statistics.mean(acc[name][c]) for c in names if c in acc[name]}
+        lines.append("%s %s" % (short, " ".join("%s=%.4g" % (c, v) for c, v in means.items())))
+        d = derived_counters(means)
+        if d:
+            lines.append("  derived %s" % d)
     return "\n".join(lines)
 
 
