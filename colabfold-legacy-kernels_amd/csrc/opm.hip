@@ -131,6 +131,9 @@ __global__ __launch_bounds__(256) void opm_update_kernel(OpmUpdateArgs a) {
 
 constexpr int kOpmRows = 16, kOpmE = 32, kOpmB = 16, kOpmD = 4, kOpmChunk = 16;
 constexpr int kLtLd = kOpmRows + 4;  // Lt[c][b][a] row stride (halfs), 8-byte aligned rows
+// Lt channel stride (halfs): 4 halfs past the 16 rows, so that channels 8 apart (the two 8-channel
+// halves a staging store instruction writes) fall on different LDS banks
+constexpr int kLtCh = kOpmB * kLtLd + 4;
 
 struct OpmOuterArgs {
     const half_t *left, *right, *wT;  // left [16, B, C], right [16, D, 32], wT [F, 32 C]
@@ -148,7 +151,7 @@ template <int F, int DPW>
 __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
     constexpr int FB = F / 16;
     constexpr int kWLd = kOpmE + 8;  // Ws row stride (halfs)
-    __shared__ __attribute__((aligned(16))) half_t Lt[kOpmChunk * kOpmB * kLtLd];
+    __shared__ __attribute__((aligned(16))) half_t Lt[kOpmChunk * kLtCh];
     __shared__ __attribute__((aligned(16))) half_t Ws[2][2][F * kWLd];  // [buffer][channel of the pair]
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
@@ -172,9 +175,7 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
     // instead of being waited for at once.
     constexpr int WCH = F * (kOpmE / 8);                        // 16-byte weight chunks per channel
     constexpr int WCPT = (WCH + 255) / 256;                     // per thread
-    constexpr int LCPT = kOpmRows * kOpmB * (kOpmChunk / 8) / 256;  // left chunks per thread
-    static_assert(kOpmRows * kOpmB * (kOpmChunk / 8) % 256 == 0, "whole left chunks per thread");
-    half8 wreg[2][WCPT], lreg[LCPT];
+    half8 wreg[2][WCPT], lreg[2];
     // channels c and c + 1 (a pair: C is a multiple of 16)
     const auto fetch_w = [&](int c) {
 #pragma unroll
@@ -198,23 +199,22 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
                 }
             }
     };
-    // rows b past B repeat the last row (their results are not stored)
+    // The first product's B operand gives lane (b, g) rows a = 4 g .. +3 of one channel and row b:
+    // 8 bytes at Lt[c][b][4 g]. So a thread stages rows a = 2 lp and 2 lp + 1 of row b = lb for the
+    // eight channels of half lv of the chunk (two 16-byte loads, consecutive lanes covering the two
+    // halves of a 32-byte run of a row) and writes each channel's two values as one 4-byte store.
+    // Rows b past B repeat the last row (their results are not stored).
+    static_assert(kOpmRows / 2 * kOpmB * (kOpmChunk / 8) == 256, "one (row pair, row b, half) per thread");
+    const int lv = tid & 1, lb = (tid >> 1) & (kOpmB - 1), lp = tid >> 5;
     const auto fetch_left = [&](int c0) {
-#pragma unroll
-        for (int u = 0; u < LCPT; ++u) {
-            const int i = tid + 256 * u;
-            const int v = i % (kOpmChunk / 8), b = i / (kOpmChunk / 8) % kOpmB, r = i / (kOpmChunk / 8) / kOpmB;
-            lreg[u] = *reinterpret_cast<const half8*>(a.left + ((int64_t)r * a.B + min(b0 + b, a.B - 1)) * a.C + c0 + 8 * v);
-        }
+        const half_t* src = a.left + ((int64_t)(2 * lp) * a.B + min(b0 + lb, a.B - 1)) * a.C + c0 + 8 * lv;
+        lreg[0] = *reinterpret_cast<const half8*>(src);
+        lreg[1] = *reinterpret_cast<const half8*>(src + (int64_t)a.B * a.C);
     };
     const auto store_left = [&]() {
+        half_t* dst = &Lt[8 * lv * kLtCh + lb * kLtLd + 2 * lp];
 #pragma unroll
-        for (int u = 0; u < LCPT; ++u) {
-            const int i = tid + 256 * u;
-            const int v = i % (kOpmChunk / 8), b = i / (kOpmChunk / 8) % kOpmB, r = i / (kOpmChunk / 8) / kOpmB;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) Lt[((8 * v + j) * kOpmB + b) * kLtLd + r] = lreg[u][j];
-        }
+        for (int j = 0; j < 8; ++j) *reinterpret_cast<half2v*>(dst + j * kLtCh) = half2v{lreg[0][j], lreg[1][j]};
     };
 
     float4v acc[DPW][FB];
@@ -240,13 +240,13 @@ __global__ __launch_bounds__(256) void opm_outer_kernel(OpmOuterArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             // G^T[e][b] for channel c + h: B operand L^T (lane column b, k-slots a = 4 g .. 4 g + 3)
-            const half4 lb = *reinterpret_cast<const half4*>(&Lt[((cl + h) * kOpmB + r16) * kLtLd + 4 * g]);
+            const half4 lbop = *reinterpret_cast<const half4*>(&Lt[(cl + h) * kLtCh + r16 * kLtLd + 4 * g]);
             half8 gop[DPW];
 #pragma unroll
             for (int dj = 0; dj < DPW; ++dj)
 #pragma unroll
                 for (int eb = 0; eb < 2; ++eb) {
-                    const float4v gt = mfma16x16x16(ra[dj][eb], lb, float4v{0.f, 0.f, 0.f, 0.f});
+                    const float4v gt = mfma16x16x16(ra[dj][eb], lbop, float4v{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                     for (int i = 0; i < 4; ++i) gop[dj][4 * eb + i] = (half_t)gt[i];  // the f16 outer product
                 }
