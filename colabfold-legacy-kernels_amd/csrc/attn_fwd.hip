@@ -35,9 +35,19 @@ struct FwdArgs {
     int N, H, Sq, Sk, D;
     float scale;
     int bias_vec;  // bias rows are whole 16-byte vectors (Sk % 8 == 0), one head's bias < 2^31 bytes
-    int head_major;  // work items head-major ([N,H,S,D] tensors), else row-major (packed rows)
+    int order;     // work-item order (ItemOrder)
     FastDiv fqt, fn, fh;  // division by the query tiles per (n, h), by N and by H (set at launch)
 };
+
+// Orders of the (n, h) work items, each item's query tiles consecutive. An XCD takes a contiguous
+// run of items (xcd_item), so the order decides what its L2 holds at once:
+// - kOrderHeads, head-major, for [N,H,S,D] tensors: a run covers few heads, so the bias rows it
+//   reads stay in its L2;
+// - kOrderHeadPairs, for packed rows with H even: head pairs outermost, then rows, then the two
+//   heads of the pair. A row's K/V/gate values of heads 2j and 2j + 1 share 128-byte lines (at
+//   D = 32), which the pair reads together, and a run's bias is two heads';
+// - kOrderRows, for packed rows with H odd: the heads of one row together.
+enum ItemOrder { kOrderRows = 0, kOrderHeads = 1, kOrderHeadPairs = 2 };
 
 template <int DP>
 struct FwdTile {
@@ -97,13 +107,19 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
     __shared__ __attribute__((aligned(16))) half_t Bs[T::kWaves][2][4 * 520];
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
-    // head-major order for [N,H,S,D] tensors: an XCD's contiguous run of items covers few
-    // heads, so the bias rows it reads stay in its L2; packed rows hold every head of a row n
-    // together, so there the heads of one row run together instead
     const int rest = fdiv(item, a.fqt), qt = item - rest * (int)a.fqt.d;
-    const int nh_major = fdiv(rest, a.fn), nh_minor = fdiv(rest, a.fh);
-    const int n = a.head_major ? rest - nh_major * a.N : nh_minor;
-    const int h = a.head_major ? nh_major : rest - nh_minor * a.H;
+    int n, h;
+    if (a.order == kOrderHeads) {
+        h = fdiv(rest, a.fn);
+        n = rest - h * a.N;
+    } else if (a.order == kOrderHeadPairs) {
+        const int pair = fdiv(rest >> 1, a.fn);
+        n = (rest >> 1) - pair * a.N;
+        h = 2 * pair + (rest & 1);
+    } else {
+        n = fdiv(rest, a.fh);
+        h = rest - n * a.H;
+    }
     const int q0 = qt * T::kBQ;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int r16 = lane & 15, g = lane >> 4;
@@ -203,15 +219,46 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         const auto rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mrow + k0), 0, rows, 0x00020000);
         mbyte = __builtin_amdgcn_raw_buffer_load_b8(rm, (uint32_t)lane, 0, 0);
     };
-    const auto stage = [&](int buf, uint64_t keep) {
+    // Dead keys of a tile whose bias came through LDS, when they are few: each takes its logit in
+    // the wave's own bias tile before the tile's reads, one LDS store per key from the wave's
+    // first 32 lanes (one query row each) in a scalar loop over the keys (the keep ballot is
+    // uniform): the masked logit inside Sk, -inf past it. Tiles with more dead keys fix the bias
+    // registers instead (fix_bias, a fixed cost per tile). At DP = 32 the stores go with the
+    // tile's K zeroing, in stage's wait for the tile's loads (a branch that only tiles with a
+    // dead key take), so a tile loop without dead keys carries none of this code; other widths
+    // store at the start of the tile, after its wait for the bias loads.
+    typedef __attribute__((address_space(3))) char lds_char;
+    const auto kill_bias_lds = [&](int bb, int k0, uint64_t keep64) {
+        if (lane >= 32) return;
+        const int kvalid = a.Sk - k0;
+        const uint64_t inside = kvalid >= 64 ? ~0ull : (1ull << kvalid) - 1ull;
+        // (the lane's row base and swizzle, formed here rather than kept live through the kernel)
+        lds_char* const row = (lds_char*)(&Bs[wv][bb][0]) + 1040 * ((lane & 31) >> 3) + 128 * (lane & 7);
+        const uint32_t kill_x = 32u * (uint32_t)((lane & 7) >> 1);
+        const auto put = [&](uint64_t keys, half_t v) {
+            while (keys) {
+                const uint32_t k = (uint32_t)__builtin_ctzll(keys);
+                keys &= keys - 1ull;
+                *reinterpret_cast<__attribute__((address_space(3))) half_t*>(row + ((2u * k) ^ kill_x)) = v;
+            }
+        };
+        put(~keep64 & inside, (half_t)kMaskedLogit);
+        put(~keep64 & ~inside, (half_t)(-INFINITY));
+    };
+    constexpr int kKillMax = 8;  // most dead keys per tile that go through LDS stores
+    const auto stage = [&](auto vec, int buf, int k0, uint64_t keep) {
         if constexpr (DP == 32) {
             // the tile came by direct-to-LDS loads (below): once they have landed, each wave
-            // zeroes the K rows of the masked keys in its own fragment block
+            // zeroes the K rows of the masked keys in its own fragment block, and where its bias
+            // came through LDS too, writes a few dead keys' logits into its bias tile
             if (keep != ~0ull) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 const int key = 16 * ((lane & 15) >> 2) + 4 * wv + (lane & 3);
                 if (!((keep >> key) & 1u))
                     *reinterpret_cast<half8*>((buf ? K32b : K32a) + 512 * wv + 8 * lane) = zero8();
+                if constexpr (decltype(vec)::value) {
+                    if (__builtin_popcountll(~keep) <= kKillMax) kill_bias_lds(buf, k0, keep);
+                }
             }
         } else {
             half_t* Ks = Ks2[buf];
@@ -311,30 +358,6 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             b[qb].hi = ld8(p + 8);
         }
     };
-    // Dead keys of a tile whose bias came through LDS, when they are few: each takes its logit in
-    // the wave's own bias tile before the tile's reads, one LDS store per key from the wave's
-    // first 32 lanes (one query row each) in a scalar loop over the keys (the keep ballot is
-    // uniform): the masked logit inside Sk, -inf past it. Tiles with more dead keys fix the bias
-    // registers instead (fix_bias, a fixed cost per tile).
-    typedef __attribute__((address_space(3))) char lds_char;
-    lds_char* const kill_row = (lds_char*)(&Bs[wv][0][0]) + 1040 * ((lane & 31) >> 3) + 128 * (lane & 7);
-    const uint32_t kill_x = 32u * (uint32_t)((lane & 7) >> 1);
-    const auto kill_bias_lds = [&](int bb, int k0, uint64_t keep64) {
-        if (lane >= 32) return;
-        const int kvalid = a.Sk - k0;
-        const uint64_t inside = kvalid >= 64 ? ~0ull : (1ull << kvalid) - 1ull;
-        lds_char* const row = kill_row + bb * (int)sizeof(Bs[0][0]);
-        const auto put = [&](uint64_t keys, half_t v) {
-            while (keys) {
-                const uint32_t k = (uint32_t)__builtin_ctzll(keys);
-                keys &= keys - 1ull;
-                *reinterpret_cast<__attribute__((address_space(3))) half_t*>(row + ((2u * k) ^ kill_x)) = v;
-            }
-        };
-        put(~keep64 & inside, (half_t)kMaskedLogit);
-        put(~keep64 & ~inside, (half_t)(-INFINITY));
-    };
-    constexpr int kKillMax = 8;  // most dead keys per tile that go through LDS stores
     const auto fetch_bias = [&](int k0, H16 (&b)[T::kQB]) {
         if (a.bias_vec && k0 + T::kBK <= a.Sk) {
 #pragma unroll
@@ -380,17 +403,20 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         const half_t* Vs = DP == 32 ? (buf ? V32b : V32a) : Vs2[buf & (DP == 32 ? 0 : 1)];
         bool more = true;
         bool reg_fix = keep_cur != ~0ull;
+        int k_next = k0 + T::kBK;
         if constexpr (decltype(vec)::value) {
             // this tile's bias loads, issued a tile ago, are the only loads in flight: wait for
             // them (the compiler does not order LDS reads after direct-to-LDS loads by itself)
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             // (keys past Sk read as dead: their mask bytes load as zero)
             reg_fix = keep_cur != ~0ull && __builtin_popcountll(~keep_cur) > kKillMax;
-            if (keep_cur != ~0ull && !reg_fix) kill_bias_lds(buf, k0, keep_cur);
+            if constexpr (DP != 32) {
+                if (keep_cur != ~0ull && !reg_fix) kill_bias_lds(buf, k0, keep_cur);
+            }
             read_bias(buf, bias16);
-            const int kn = min(k0 + T::kBK, k_last);
-            fetch_kv(kn, buf ^ 1);
-            dma_bias(kn, buf ^ 1);
+            k_next = min(k0 + T::kBK, k_last);
+            fetch_kv(k_next, buf ^ 1);
+            dma_bias(k_next, buf ^ 1);
         } else {
             more = k0 + T::kBK < k_end;
             if (more) {
@@ -525,7 +551,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         // the other buffer was last read a tile ago, before the barrier that ended that tile
         if (more) {
             keep_cur = __ballot(mbyte != 0u);
-            stage(buf ^ 1, keep_cur);
+            stage(vec, buf ^ 1, k_next, keep_cur);
         }
         // at DP = 32 the next tile's K and V, loaded straight into LDS at the start of this tile,
         // have landed before the barrier after which every wave reads them (the compiler also
@@ -545,7 +571,7 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         }
         load_q();
         keep_cur = __ballot(mbyte != 0u);
-        stage(0, keep_cur);
+        stage(vec, 0, 0, keep_cur);
         __syncthreads();
         tile(vec, std::true_type{}, 0, 0, biasA, biasB);
         for (int k0 = T::kBK; k0 < k_end; k0 += 2 * T::kBK) {
@@ -659,7 +685,7 @@ static FwdArgs contiguous_args(int N, int H, int Sq, int Sk, int D) {
     a.Sq = Sq;
     a.Sk = Sk;
     a.D = D;
-    a.head_major = 1;
+    a.order = kOrderHeads;
     return a;
 }
 
@@ -755,6 +781,7 @@ static int packed_common(clk_stream stream, int32_t device, const clk_buffer* p,
     a.lse = nullptr;
     a.scale = scale;
     a.bias_vec = S % 8 == 0 && aligned16(a.bias) && (int64_t)S * S * 2 < ((int64_t)1 << 31);
+    a.order = H % 2 == 0 ? kOrderHeadPairs : kOrderRows;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (lims) {
         return G == 4 ? dispatch_fwd<false, true, true>(s, device, a)

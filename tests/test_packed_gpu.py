@@ -2,7 +2,8 @@
 
 Cases are the reference's tests/test_packed_attention.py:88-93 (X, Y, H, D, column, masked
 fraction, live length): rows and columns, D from 8 to 64, lengths that are and are not
-multiples of 8, and live < S (trim). Inputs as its one() (60-71): p ~ N(0,1), bias ~ N(0,1),
+multiples of 8, and live < S (trim); plus two cases with an odd head count, which the kernel
+orders row by row instead of by head pairs. Inputs as its one() (60-71): p ~ N(0,1), bias ~ N(0,1),
 gate_bias ~ 0.1 N(0,1), a padded tail and a dead last row when live < S.
 
 Checks (fp16 I/O): every batch row against the oracle, which shares the kernels' -1e4 mask
@@ -29,7 +30,8 @@ CASES = ((384, 384, 4, 32, False, 0.01, 384), (96, 384, 8, 32, True, 0.01, 96),
          (3, 37, 4, 32, True, 0.2, 3), (4, 264, 4, 32, False, 0.05, 264),
          (5, 129, 4, 32, True, 0.5, 5), (6, 256, 4, 32, False, 0.05, 200),
          (256, 6, 4, 32, True, 0.05, 200), (4, 128, 8, 8, False, 0.05, 72),
-         (4, 261, 4, 32, False, 0.05, 200))
+         (4, 261, 4, 32, False, 0.05, 200),
+         (8, 96, 3, 32, False, 0.05, 96), (96, 8, 5, 16, True, 0.05, 80))
 
 
 def make(X, Y, H, D, column, frac, live, G=4):
