@@ -15,8 +15,11 @@ VoltaMmaBwd(want_dbias), through the library's C ABI on the current stream, inpu
 HBM. value is the step's algorithmic TFLOP/s (14 u flops, u = N H S^2 D: forward 4u, backward
 10u with its recompute of S). The other GPU configs of BASELINE.json are reported beside it as
 objects of the same line: "c2" (triangle attention fwd + bwd, N_res = 256) and "c5" (triangle
-attention forward, N_res = 1024, want_lse off), each with its kernels and roofline. Per-kernel durations come from HIP events that the library records
-on its launch stream at its kernel boundaries (clk_set_stage_events); the roofline object is the
+attention forward, N_res = 1024, want_lse off), each with its kernels and roofline. ms_per_step
+is timed over steps launched back to back with nothing else in the stream; per-kernel durations
+come from as many more steps with HIP events that the library records on its launch stream at
+its kernel boundaries (clk_set_stage_events), whose own step time is ms_per_step_staged (each
+event record adds a few microseconds of device time). The roofline object is the
 dominant kernel's, its "traffic" the HBM bytes per dispatch that the committed rocprofv3 counter
 summaries (profiles/attention_c3_traffic.txt, profiles/attention_c2_c5_traffic.txt) measured for
 that kernel at that config. Reported beside the step:
@@ -105,9 +108,11 @@ def disarm(hip):
     hip.lib().clk_set_stage_events(None, 0)
 
 
-def roof_entry(ms_list, flops, byts, **extra):
-    """Per-kernel timing against both roofs; the bound is the larger ideal time."""
-    mean, med = statistics.mean(ms_list), statistics.median(ms_list)
+def roof_entry(ms_list, flops, byts, mean=None, **extra):
+    """Per-kernel timing against both roofs; the bound is the larger ideal time. `mean` replaces
+    the mean of ms_list where the caller timed the calls another way."""
+    med = statistics.median(ms_list)
+    mean = statistics.mean(ms_list) if mean is None else mean
     t_mfma = flops / (PEAK_TFLOPS * 1e12) * 1e3
     t_hbm = byts / (PEAK_GBS * 1e9) * 1e3
     e = {"ms": round(mean, 5), "ms_median": round(med, 5), "calls": len(ms_list),
@@ -183,7 +188,11 @@ def attention_sets(torch, hip, n, h, s, d, mask_frac, bias_std, seed, backward, 
 def bench_attention(torch, hip, steps, warmup, ev, n=N, h=H, s=S, d=D, mask_frac=0.0, bias_std=1.0,
                     seed=0, backward=True, want_lse=True):
     """ms per step (VoltaMma, then VoltaMmaBwd(want_dbias) when `backward`), the step's
-    algorithmic flops, and per-kernel timings from the library's stage events."""
+    algorithmic flops, per-kernel timings from the library's stage events, and ms per step with
+    those events armed. The step time comes from `steps` steps launched back to back between two
+    events, with no stage events in the stream (each event record the library makes at a kernel
+    boundary adds a few microseconds of device time); the per-kernel timings from `steps` more
+    steps with them armed."""
     u = float(n) * h * s * s * d
     scale = d ** -0.5
     sets = attention_sets(torch, hip, n, h, s, d, mask_frac, bias_std, seed, backward, want_lse)
@@ -204,17 +213,23 @@ def bench_attention(torch, hip, steps, warmup, ev, n=N, h=H, s=S, d=D, mask_frac
     bwd_stages = BWD_STAGES if backward else ()
     for i in range(warmup):
         step(sets[i % 2])
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        step(sets[i % 2])
+    stop.record()
+    torch.cuda.synchronize()
+    plain_ms = start.elapsed_time(stop)
     fwd_evs = [ev.create(len(FWD_STAGES) + 1) for _ in range(steps)]
     bwd_evs = [ev.create(len(bwd_stages) + 1) if backward else None for _ in range(steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for i in range(steps):
         step(sets[i % 2], fwd_evs[i], bwd_evs[i])
     stop.record()
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
+    staged_ms = start.elapsed_time(stop)
     per = {name: [] for name in FWD_STAGES + bwd_stages}
     for fe, be in zip(fwd_evs, bwd_evs):
         for i, name in enumerate(FWD_STAGES):
@@ -229,7 +244,7 @@ def bench_attention(torch, hip, steps, warmup, ev, n=N, h=H, s=S, d=D, mask_frac
     algo = attention_algo(ws_bytes, n, h, s, d)
     kernels = {name: roof_entry(per[name], algo[name][0], algo[name][1], scratch_bytes=algo[name][2])
                for name in per}
-    return total_ms / steps, (14 if backward else 4) * u, kernels
+    return plain_ms / steps, (14 if backward else 4) * u, kernels, staged_ms / steps
 
 
 def roofline_of(kernels, prefix=""):
@@ -263,11 +278,12 @@ EXTRA_CONFIGS = {
 def bench_extra(torch, hip, ev, name, steps, warmup):
     cfg = dict(EXTRA_CONFIGS[name])
     workload = cfg.pop("workload")
-    ms, flops, kernels = bench_attention(torch, hip, steps, warmup, ev, **cfg)
+    ms, flops, kernels, staged = bench_attention(torch, hip, steps, warmup, ev, **cfg)
     t_mfma = flops / (PEAK_TFLOPS * 1e12) * 1e3
     torch.cuda.empty_cache()
     return {"workload": workload, "shape": [cfg["n"], cfg["h"], cfg["s"], cfg["d"]],
-            "ms_per_step": round(ms, 5), "tflops": round(flops / ms / 1e9, 2),
+            "ms_per_step": round(ms, 5), "ms_per_step_staged": round(staged, 5),
+            "tflops": round(flops / ms / 1e9, 2),
             "frac_mfma_step": round(t_mfma / ms, 4), "flops_per_step": flops,
             "roofline": roofline_of(kernels, name + ":"), "kernels": kernels}
 
@@ -285,10 +301,9 @@ def bench_packed(torch, hip, iters, warmup, ev):
         gate_bias = torch.zeros(H * D, dtype=torch.float16, device="cuda")
         out = torch.empty((N, S, H, D), dtype=torch.float16, device="cuda")
         sets.append((p, bias, kmask, gate_bias, out))
-    for i in range(warmup):
-        p, bias, kmask, gb, out = sets[i % 2]
-        hip.attention_packed(p, bias, kmask, gb, D ** -0.5, out=out)
-    torch.cuda.synchronize()
+    calls = [lambda st=st: hip.attention_packed(st[0], st[1], st[2], st[3], D ** -0.5, out=st[4])
+             for st in sets]
+    plain = time_calls(torch, calls, iters, warmup)
     evs = [ev.create(2) for _ in range(iters)]
     for i in range(iters):
         p, bias, kmask, gb, out = sets[i % 2]
@@ -300,7 +315,10 @@ def bench_packed(torch, hip, iters, warmup, ev):
     for e in evs:
         ev.destroy(e)
     t = N * H * S * D * 2
-    return roof_entry(ms, 4 * u, 4 * t + H * S * S * 2 + N * S + t + H * D * 2)
+    # ms: calls back to back with no events between them; ms_median and ms_staged: per call,
+    # with the library's stage events armed
+    return roof_entry(ms, 4 * u, 4 * t + H * S * S * 2 + N * S + t + H * D * 2,
+                      mean=statistics.mean(plain), ms_staged=round(statistics.mean(ms), 5))
 
 
 def fused_bytes_flops(op, m, c, n=None, heads=0):
@@ -709,7 +727,7 @@ def main():
         print(json.dumps({args.only: bench_extra(torch, hip, ev, args.only, args.steps, args.warmup)}),
               flush=True)
         return
-    ms_step, flops_step, kernels = bench_attention(torch, hip, args.steps, args.warmup, ev)
+    ms_step, flops_step, kernels, ms_staged = bench_attention(torch, hip, args.steps, args.warmup, ev)
     roof = roofline_of(kernels)
     line = {
         "metric": METRIC,
@@ -726,7 +744,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": "C3: MSA row attention with pair bias, fwd (want_lse) + bwd (want_dbias)",
                    "N_seq": N, "N_res": S, "heads": H, "head_dim": D, "flops_per_step": flops_step,
-                   "frac_mfma_step": round(flops_step / ms_step / 1e9 / PEAK_TFLOPS, 4)},
+                   "frac_mfma_step": round(flops_step / ms_step / 1e9 / PEAK_TFLOPS, 4),
+                   "ms_per_step_staged": round(ms_staged, 5)},
         "roofline": roof,
         "kernels": kernels,
     }
