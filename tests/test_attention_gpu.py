@@ -104,6 +104,34 @@ def test_sparse_dead_keys(hip, sk, frac):
     check(got, ref, "sk=%d frac=%.2f" % (sk, frac))
 
 
+def random_case(i):
+    """Seeded shape i of the sweep: a forward config of the reference's table, Sq and Sk from 1
+    to 300 (so Sk % 8 and Sk % 64 take every kind of value: the bias-through-LDS path and the
+    register path, whole and ragged key tiles), a masked fraction from none to nearly all, and
+    n h Sq Sk bounded so the float64 oracle stays quick."""
+    rng = np.random.default_rng(1000 + i)
+    d, bq, bk = FWD_CONFIGS[int(rng.integers(len(FWD_CONFIGS)))]
+    sq, sk = (int(x) for x in rng.integers(1, 301, size=2))
+    n, h = int(rng.integers(1, 5)), int(rng.integers(1, 4))
+    while n * h * sq * sk > 400_000:
+        n, h = max(1, n // 2), max(1, h - 1) if n == 1 else h
+        if n == 1 and h == 1:
+            break
+    frac = float(rng.choice([0.0, 0.05, 0.3, 0.9]))
+    return dict(n=n, h=h, sq=sq, sk=sk, d=d, bq=bq, bk=bk, frac=frac, seed=2000 + i)
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_shapes(hip, i):
+    """A seeded sweep beyond the reference's fixed cases, against the oracle with the same bars."""
+    c = random_case(i)
+    rng = np.random.default_rng(c["seed"])
+    km = (rng.random((c["n"], c["sk"])) >= c["frac"]).astype(np.uint8)
+    got, ref = run(hip, n=c["n"], h=c["h"], sq=c["sq"], sk=c["sk"], d=c["d"], seed=c["seed"],
+                   bq=c["bq"], bk=c["bk"], kmask=km)
+    check(got, ref, "random %d %s" % (i, c))
+
+
 def test_all_masked_row(hip):
     """A batch element with every key masked: a uniform softmax, finite lse, zero dS."""
     km = np.ones((3, 96), np.uint8)
