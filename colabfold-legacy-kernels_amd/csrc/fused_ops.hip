@@ -1565,18 +1565,24 @@ __global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(T
         }
     };
     const auto gemm_store = [&](int t) {
+        // both products start from their biases: paired block b gives lane group g the rows
+        // 32 (b / 2) + 8 g + 4 (b % 2) .. +3 (output channels of W2's blocks, hidden units of W1's)
         float4v acc[NCB][RB];
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb)
+        for (int cb = 0; cb < NCB; ++cb) {
+            const float4v b2q = *reinterpret_cast<const float4v*>(b2s + 32 * (cb >> 1) + 8 * g + 4 * (cb & 1));
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+            for (int rb = 0; rb < RB; ++rb) acc[cb][rb] = b2q;
+        }
         const float* b1l = b1s + 8 * g;
         for (int p = 0; p < KH; ++p) {
             float4v hacc[2][RB];
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2)
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const float4v b1q = *reinterpret_cast<const float4v*>(b1l + 32 * p + 4 * h2);
 #pragma unroll
-                for (int rb = 0; rb < RB; ++rb) hacc[h2][rb] = float4v{0.f, 0.f, 0.f, 0.f};
+                for (int rb = 0; rb < RB; ++rb) hacc[h2][rb] = b1q;
+            }
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -1587,13 +1593,12 @@ __global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(T
                 }
             // (one product's fragment reads in flight at a time: hoisting more costs registers)
             __builtin_amdgcn_sched_barrier(0);
-            // relu(. + b1), fp16: slot 8 g + e of step p is hidden unit 32 p + 8 g + e
+            // relu, fp16: slot 8 g + e of step p is hidden unit 32 p + 8 g + e
             half8 hop[RB];
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    hop[rb][e] = (half_t)fmaxf(hacc[e >> 2][rb][e & 3] + b1l[32 * p + e], 0.f);
+                for (int e = 0; e < 8; ++e) hop[rb][e] = (half_t)fmaxf(hacc[e >> 2][rb][e & 3], 0.f);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
@@ -1616,7 +1621,7 @@ __global__ __launch_bounds__(kTransRowsThreads, 4) void transition_rows_kernel(T
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float res = ADD ? act_get<BF>(xr[rb][cp], e) : 0.f;
-                    o[e] = act_cvt<BF>(acc[2 * cp + (e >> 2)][rb][e & 3] + b2s[col + e] + res);
+                    o[e] = act_cvt<BF>(acc[2 * cp + (e >> 2)][rb][e & 3] + res);
                 }
                 // a padding tile stores zeros (with add_input it stores nothing)
                 const u32x4 ov = !ADD && work == kPadding ? u32x4{0u, 0u, 0u, 0u} : __builtin_bit_cast(u32x4, o);
