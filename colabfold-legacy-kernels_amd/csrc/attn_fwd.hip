@@ -560,6 +560,61 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         __syncthreads();
     };
 
+    // A row whose first key tile holds no live key may hold none at all: then every key inside Sk
+    // has the masked logit, the softmax is uniform, and the tile loop would produce out = the mean
+    // of the row's V rows and lse2 = -1e4 log2 e + log2 Sk. Such a workgroup (rows of padded
+    // residues) sums V instead: wave w takes rows r16 + 16 (w + 4 i), lane group g its d's, and
+    // the waves' sums meet in their own LDS bias buffers; the epilogue then divides by l = Sk.
+    const auto dead_row = [&]() -> bool {
+        bool live = false;
+        for (int k = T::kBK + lane; k < a.Sk; k += kWave) live |= mrow[k] != 0;
+        return !__any(live);
+    };
+    const auto dead_row_sums = [&]() {
+        float sv[DP / 4];
+#pragma unroll
+        for (int e = 0; e < DP / 4; ++e) sv[e] = 0.f;
+        const int range = __builtin_amdgcn_readfirstlane(a.Sk * (int)a.ks * 2);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb_base), 0, range, 0x00020000);
+        for (int k = r16 + 16 * wv; k < a.Sk; k += 16 * T::kWaves) {
+#pragma unroll
+            for (int c = 0; c < DP / 32; ++c) {
+                const int d0 = (DP / 4) * g + 8 * c;
+                const uint32_t off = d0 < a.D ? (uint32_t)((k * a.ks + d0) * 2) : 0x80000000u;
+                const half8 v = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sv[8 * c + j] += (float)v[j];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < DP / 4; ++e)
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) sv[e] += __shfl_xor(sv[e], m);
+        // the first tile's loads into this wave's LDS have landed before its buffer takes the sums
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        if (r16 == 0) {
+#pragma unroll
+            for (int e = 0; e < DP / 4; ++e) reinterpret_cast<float*>(&Bs[wv][0][0])[(DP / 4) * g + e] = sv[e];
+        }
+        __syncthreads();
+        float tot[DP / 4];
+#pragma unroll
+        for (int e = 0; e < DP / 4; ++e) {
+            tot[e] = 0.f;
+#pragma unroll
+            for (int w = 0; w < T::kWaves; ++w) tot[e] += reinterpret_cast<const float*>(&Bs[w][0][0])[(DP / 4) * g + e];
+        }
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+#pragma unroll
+            for (int db = 0; db < T::kDB; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[db][qb][i] = tot[4 * db + i];
+            l_run[qb] = g == 0 ? (float)a.Sk : 0.f;
+            m_run[qb] = kMaskedLogit;
+        }
+    };
+
     H16 biasA[T::kQB], biasB[T::kQB];
     const auto run = [&](auto vec) __attribute__((always_inline)) {
         fetch_kv(0, 0);
@@ -571,6 +626,12 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         }
         load_q();
         keep_cur = __ballot(mbyte != 0u);
+        if constexpr (!TRIM) {
+            if (keep_cur == 0ull && dead_row()) {
+                dead_row_sums();
+                return;
+            }
+        }
         stage(vec, 0, 0, keep_cur);
         __syncthreads();
         tile(vec, std::true_type{}, 0, 0, biasA, biasB);

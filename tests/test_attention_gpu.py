@@ -132,15 +132,20 @@ def test_random_shapes(hip, i):
     check(got, ref, "random %d %s" % (i, c))
 
 
-def test_all_masked_row(hip):
-    """A batch element with every key masked: a uniform softmax, finite lse, zero dS."""
-    km = np.ones((3, 96), np.uint8)
+@pytest.mark.parametrize("d,sk,bk", [(32, 96, 32), (32, 40, 32), (32, 200, 64), (8, 130, 32),
+                                     (64, 136, 64), (96, 100, 32)])
+def test_all_masked_row(hip, d, sk, bk):
+    """A batch element with every key masked: a uniform softmax, finite lse, zero dS. The
+    forward takes such a row's closed form (the mean of its V rows) once its first key tile
+    shows no live key and the rest of its mask none either; Sk <= 64 has only that tile."""
+    km = np.ones((3, sk), np.uint8)
     km[1, :] = 0
-    got, ref = run(hip, kmask=km)
-    check(got, ref, "all-masked")
+    km[2, 70:] = 0  # a live first tile, dead keys after it: the tile loop
+    got, ref = run(hip, sk=sk, d=d, bk=bk, kmask=km)
+    check(got, ref, "all-masked d=%d sk=%d" % (d, sk))
     # the closed form: out = mean of v, lse2 = log2(Sk) - 1e4 log2(e)
     lse_row = got["lse"][1]
-    assert np.allclose(lse_row, np.log2(96) + ora.MASKED_LOGIT * ora.LOG2E, atol=2e-3)
+    assert np.allclose(lse_row, np.log2(sk) + ora.MASKED_LOGIT * ora.LOG2E, atol=2e-3)
 
 
 @pytest.mark.parametrize("d,bq,bk", FWD_CONFIGS)
