@@ -305,6 +305,27 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             fetch(k0);
         }
     };
+    // Gated at DP = 32: the last key tile loads, in place of a next tile, the wave's gate rows into
+    // the idle buffer's regions of this wave (its K fragment block: query block 0, its V rows:
+    // block 1), so the epilogue's gate reads are LDS reads whose memory latency the last tile
+    // covered. Slot l of block qb is query q0w + 16 qb + R (R = l / 4), 16-byte chunk
+    // c = (l % 4) ^ (R / 4) % 4 of the row, at byte 16 l; rows past Sq and chunks past D read zeros.
+    bool gate_lds = false;
+    const auto dma_gate = [&](int buf) {
+        const int R = lane >> 2, c = (lane & 3) ^ ((R >> 2) & 3);
+        const int rows = max(a.Sq - q0w, 0);
+        const int range = __builtin_amdgcn_readfirstlane(min(rows, T::kQB * 16) * (int)a.qs * 2);
+        const auto rg = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.gate + qbase + (int64_t)q0w * a.qs),
+                                                          0, range, 0x00020000);
+#pragma unroll
+        for (int qb = 0; qb < T::kQB; ++qb) {
+            const uint32_t off = 8 * c < a.D ? (uint32_t)(((16 * qb + R) * a.qs + 8 * c) * 2) : 0x80000000u;
+            half_t* dst = (qb == 0 ? (buf ? K32b : K32a) : (buf ? V32b : V32a)) + 512 * wv;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
+        }
+        gate_lds = true;
+    };
+    int gate_buf = 0;
 
     // bias of this lane's 16 keys k0 + 16 g .. +15 for its queries, in a register set per tile
     // parity: loaded one key tile ahead where rows are not whole 16-byte vectors, else read from
@@ -415,13 +436,22 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             }
             read_bias(buf, bias16);
             k_next = min(k0 + T::kBK, k_last);
-            fetch_kv(k_next, buf ^ 1);
-            dma_bias(k_next, buf ^ 1);
+            if (GATE && DP == 32 && k0 == k_last) {
+                dma_gate(buf ^ 1);
+                gate_buf = buf ^ 1;
+                more = false;
+            } else {
+                fetch_kv(k_next, buf ^ 1);
+                dma_bias(k_next, buf ^ 1);
+            }
         } else {
             more = k0 + T::kBK < k_end;
             if (more) {
                 fetch_kv(k0 + T::kBK, buf ^ 1);
                 fetch_bias(k0 + T::kBK, bias_next);
+            } else if constexpr (GATE && DP == 32) {
+                dma_gate(buf ^ 1);
+                gate_buf = buf ^ 1;
             }
         }
         // every key of the tile kept and inside Sk: the bias stands as loaded (through LDS a few
@@ -670,7 +700,13 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             half8 o;
             half8 gt, gb;
             if constexpr (GATE) {
-                gt = ld8(a.gate + qbase + gq * a.qs + d0);
+                if (DP == 32 && gate_lds) {
+                    // (the final wait for loads at the end of the tile loop covers the gate rows)
+                    const half_t* gl = (qb == 0 ? (gate_buf ? K32b : K32a) : (gate_buf ? V32b : V32a)) + 512 * wv;
+                    gt = ld8(gl + 32 * r16 + 8 * (g ^ ((r16 >> 2) & 3)));
+                } else {
+                    gt = ld8(a.gate + qbase + gq * a.qs + d0);
+                }
 #pragma unroll
                 for (int j = 0; j < 8; ++j) gb[j] = a.gate_bias[h * a.D + d0 + j];
             }
