@@ -323,6 +323,11 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
             half_t* dst = (qb == 0 ? (buf ? K32b : K32a) : (buf ? V32b : V32a)) + 512 * wv;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
         }
+        // and the head's gate bias (D halfs) into the wave's idle bias buffer of that parity
+        const auto rgb = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(a.gate_bias + (int64_t)h * a.D), 0,
+                                                           a.D * 2, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rgb, (__attribute__((address_space(3))) void*)&Bs[wv][buf][0], 16,
+                                                 16u * (uint32_t)lane, 0, 0, 0);
         gate_lds = true;
     };
     int gate_buf = 0;
@@ -680,7 +685,20 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
         }
     }
 
-    // epilogue: lane g holds d = (DP/4) g .. +DP/4 of query q0w + 16 qb + r16
+    // epilogue: lane g holds d = (DP/4) g .. +DP/4 of query q0w + 16 qb + r16. Gated, out =
+    // acc / (l (1 + 2^(-(gate + gate_bias) log2 e))): one reciprocal per element covers both the
+    // softmax normalisation and the sigmoid, and -gate_bias log2 e is formed once per lane.
+    float ngb[DP / 32][8];
+    if constexpr (GATE) {
+#pragma unroll
+        for (int c = 0; c < DP / 32; ++c) {
+            // (a chunk past D, never stored, reads the last chunk: the loads need no guard)
+            const int d0 = min((DP / 4) * g + 8 * c, a.D - 8);
+            const half8 gb = DP == 32 && gate_lds ? ld8(&Bs[wv][gate_buf][d0]) : ld8(a.gate_bias + h * a.D + d0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ngb[c][j] = -kLog2e * (float)gb[j];
+        }
+    }
 #pragma unroll
     for (int qb = 0; qb < T::kQB; ++qb) {
         const int gq = q0w + 16 * qb + r16;
@@ -692,13 +710,14 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
                     l > 0.f ? m_run[qb] * kLog2e + log2f(l) : -INFINITY;
             }
         }
-        const float inv = __builtin_amdgcn_rcpf(fmaxf(l, 1e-30f));
+        const float lc = fmaxf(l, 1e-30f);
+        const float inv = GATE ? 0.f : __builtin_amdgcn_rcpf(lc);
 #pragma unroll
         for (int c = 0; c < DP / 32; ++c) {
             const int d0 = (DP / 4) * g + 8 * c;
             if (d0 >= a.D) continue;
             half8 o;
-            half8 gt, gb;
+            half8 gt;
             if constexpr (GATE) {
                 if (DP == 32 && gate_lds) {
                     // (the final wait for loads at the end of the tile loop covers the gate rows)
@@ -707,14 +726,17 @@ __global__ __launch_bounds__(FwdTile<DP>::kThreads, DP == 32 ? 3 : 1) void attn_
                 } else {
                     gt = ld8(a.gate + qbase + gq * a.qs + d0);
                 }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) gb[j] = a.gate_bias[h * a.D + d0 + j];
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int db = 2 * c + j / 4, i = j & 3;
-                float val = acc[db][qb][i] * inv;
-                if constexpr (GATE) val *= sigmoid_fast((float)gt[j] + (float)gb[j]);
+                float val;
+                if constexpr (GATE) {
+                    const float e = exp2_fast(fmaf((float)gt[j], -kLog2e, ngb[c][j]));
+                    val = acc[db][qb][i] * __builtin_amdgcn_rcpf(fmaf(lc, e, lc));
+                } else {
+                    val = acc[db][qb][i] * inv;
+                }
                 o[j] = (half_t)val;
             }
             *reinterpret_cast<half8*>(a.out + obase + gq * a.os + d0) = o;
