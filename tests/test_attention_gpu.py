@@ -104,6 +104,35 @@ def test_sparse_dead_keys(hip, sk, frac):
     check(got, ref, "sk=%d frac=%.2f" % (sk, frac))
 
 
+def run_with_bias(hip, q, k, v, bias, km, dout, d, bq=64, bk=32):
+    scale = float(d) ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale, bq, bk, want_lse=True)
+    dq, dk, dv, dbias = hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale, want_dbias=True)
+    got = dict(zip(("out", "lse", "dq", "dk", "dv", "dbias"), host(out, lse, dq, dk, dv, dbias)))
+    ref_out, ref_lse = ora.attention_fwd(q, k, v, bias, km, scale)
+    ref = dict(zip(("dq", "dk", "dv", "dbias"), ora.attention_bwd(q, k, v, bias, km, dout, scale)))
+    ref["out"], ref["lse"] = ref_out, ref_lse
+    return got, ref
+
+
+@pytest.mark.parametrize("d,sk,bk,near", [(32, 256, 32, False), (32, 250, 64, False), (64, 256, 64, False),
+                                          (8, 200, 32, False), (32, 256, 32, True), (96, 250, 32, True)])
+def test_dead_key_tiles(hip, d, sk, bk, near):
+    """Whole 64-key tiles with no live key after a live first tile (keys 64..127 and from 160 on
+    masked in every row, the last tile ragged or past Sk where Sk % 64 != 0). With `near` the
+    live keys' bias sits at -9992, 8 above the masked logit, where the masked keys still weigh
+    e^-8 against the live ones (fp32 logits near 1e4 carry about 1e-3 of rounding)."""
+    q, k, v, bias, _, dout = inputs(3, 2, 96, sk, d, 11)
+    km = np.ones((3, sk), np.uint8)
+    km[:, 64:128] = 0
+    km[:, 160:] = 0
+    if near:
+        bias = np.full_like(bias, -9992.0)
+    got, ref = run_with_bias(hip, q, k, v, bias, km, dout, d, bk=bk)
+    check(got, ref, "dead tiles d=%d sk=%d near=%s" % (d, sk, near))
+
+
 def random_case(i):
     """Seeded shape i of the sweep: a forward config of the reference's table, Sq and Sk from 1
     to 300 (so Sk % 8 and Sk % 64 take every kind of value: the bias-through-LDS path and the
