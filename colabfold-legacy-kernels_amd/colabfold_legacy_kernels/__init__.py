@@ -51,7 +51,7 @@ KERNELS = tuple(_TABLE)
 
 
 def supported_capabilities():
-    """Give the capabilities (gfx target numbers) that this package contains."""
+    """The gfx target numbers this package ships libraries for."""
     return _CAPABILITIES
 
 
@@ -62,7 +62,8 @@ def _normalise(cc):
 
 
 def _resolve(kernel, cc):
-    """Find the library and the FFI symbol for one kernel and one capability."""
+    """(cc, library file, FFI symbol) serving `kernel` at capability `cc`, None for the last two where
+    nothing does; an unknown kernel name raises KeyError."""
     if kernel not in _TABLE:
         raise KeyError(
             "unknown kernel %r, expected one of %s" % (kernel, ", ".join(KERNELS)))
@@ -76,13 +77,13 @@ def _resolve(kernel, cc):
 
 
 def kernel_dir(cc):
-    """Give the directory of the libraries for one capability."""
+    """Directory that holds the libraries built for capability `cc`."""
     cc, _, _ = _resolve("attention", cc)
     return str(_KERNEL_DIR / ("gfx%d" % cc))
 
 
 def library_path(kernel, cc):
-    """Give the path of the library that supplies one kernel."""
+    """Path to the shared library implementing `kernel` at capability `cc`."""
     cc, lib, _ = _resolve(kernel, cc)
     if lib is None:
         raise FileNotFoundError(
@@ -94,7 +95,7 @@ def library_path(kernel, cc):
 
 
 def symbol(kernel, cc):
-    """Give the XLA FFI target name that the library exports."""
+    """XLA FFI handler name under which the library exports `kernel`."""
     cc, lib, sym = _resolve(kernel, cc)
     if sym is None:
         raise FileNotFoundError(
@@ -103,7 +104,7 @@ def symbol(kernel, cc):
 
 
 def available(cc, kernel=None):
-    """Tell if the kernels are present. With kernel=None, test all of them."""
+    """True when `kernel` (or, with None, every kernel in KERNELS) has its library in place for `cc`."""
     names = KERNELS if kernel is None else (kernel,)
     for name in names:
         try:
