@@ -857,7 +857,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dkdv_kernel(BwdArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// dK, dV and the dBias partials where D == 32 and Sq <= 32 QT (QT in {4, 8, 12}): the same
+// dK, dV and the dBias partials where D == 32 and Sq <= 32 QT (QT = 4 launches it; the same
+// layout in query parts, attn_bwd_dkdv_reg3_kernel, serves QT 8 and 12): the same
 // products and lane layout as attn_bwd_dkdv_kernel, arranged so that the dBias partial never
 // leaves registers. A workgroup of eight waves owns 64 keys of one head and a chunk of batch
 // rows: wave w takes key group w % 4 (16 keys) and query half w / 4 (QT / 2 tiles of 32), so the
@@ -1146,12 +1147,14 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// The register dK/dV kernel for QT = 12 (256 < Sq <= 384, D = 32) at three waves per SIMD:
-// twelve waves per workgroup, key group w % 4 by query third w / 4 (four tiles each), so the
-// dBias partial is 32 registers per lane and the kernel fits 168 VGPRs. Its LDS holds the
-// workgroup's bias as fp16 (the original values, recovered exactly from the fp32 log2e form), so
-// s2 = log2e (scale S + bias) takes an fma with the fp16 operand read in place and a multiply.
-// The thirds' dK / dV sums meet in LDS once per row, thirds 1 and 2 into third 0 in that order.
+// The register dK/dV kernel in query parts, D = 32: for QT = 12 (256 < Sq <= 384) twelve waves
+// at three per SIMD, key group w % 4 by query third w / 4 (four tiles each, two per step), so the
+// dBias partial is 32 registers per lane and the kernel fits 168 VGPRs; for QT = 8 (128 < Sq <=
+// 256) sixteen waves at four per SIMD, key group w % 4 by query quarter w / 4 (two tiles each, one
+// per step), 16 registers of partial within 128 VGPRs. Its LDS holds the workgroup's bias as
+// fp16 (the original values, recovered exactly from the fp32 log2e form), so s2 = log2e (scale S
+// + bias) takes an fma with the fp16 operand read in place and a multiply. The parts' dK / dV
+// sums meet in LDS once per row, parts 1, 2 (, 3) into part 0 in that order.
 // The Q / dO tiles and the query terms of the next step go straight from memory into the idle
 // LDS buffer by direct-to-LDS loads (buffer_load ... lds), issued at the start of a step and
 // complete at its closing barrier: no staging registers and no LDS store instructions. The two
@@ -1159,23 +1162,34 @@ __global__ __launch_bounds__(512, 2) void attn_bwd_dkdv_reg_kernel(BwdArgs a) {
 // compiler can tell that the step's LDS reads do not alias the loads in flight and does not wait
 // for them. Everything else is attn_bwd_dkdv_reg_kernel's.
 // ------------------------------------------------------------------------------------------
-template <bool DBIAS>
-__global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
-    constexpr int DP = 32, QT = 12, TT = 4;  // tiles per third
-    constexpr int kSteps = TT / 2;
+template <int QT>
+struct PartTile {
+    static constexpr int kParts = QT == 12 ? 3 : 4;      // query parts (waves per key group)
+    static constexpr int kThreads = 4 * kParts * kWave;
+    static constexpr int kTPS = QT == 12 ? 2 : 1;        // tiles per part and step
+};
+
+template <int QT, bool DBIAS>
+__global__ __launch_bounds__(PartTile<QT>::kThreads, QT == 12 ? 3 : 4) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
+    static_assert(QT == 12 || QT == 8, "query parts of two tiles per step (QT 12) or one (QT 8)");
+    constexpr int kParts = PartTile<QT>::kParts, kTPS = PartTile<QT>::kTPS, kNT = PartTile<QT>::kThreads;
+    constexpr int DP = 32, TT = QT / kParts;  // tiles per part
+    constexpr int kSteps = TT / kTPS;
+    static_assert(kSteps == 2, "buffer parity alternates by step within a row");
     constexpr int kTile = 32 * DP, kOs = kTile + 64, kSub = kOs + kTile;
-    constexpr int kBuf = 6 * kSub;           // halfs of a step: [third][tile]
+    constexpr int kBuf = kParts * kTPS * kSub;  // halfs of a step: [part][tile]
+    constexpr int kQTerms = kParts * kTPS * 16; // float4 slots of a step's query terms
     constexpr int SqB = 32 * QT;
     constexpr int kBRow = SqB + 8;           // LDS bias row stride (halfs)
     __shared__ __attribute__((aligned(16))) half_t bias_l[65 * kBRow];  // rows: 64 keys, masked
     __shared__ __attribute__((aligned(16))) half_t lds0[kBuf];
     __shared__ __attribute__((aligned(16))) half_t lds1[kBuf];
-    // query terms of each buffer [third][tile][-lse2 / c1 x 32, -delta x 32] (384 of the first 512
-    // floats), then 384 zeros, the -delta a dead key's lane reads
+    // query terms of each buffer [part][tile][-lse2 / c1 x 32, -delta x 32] (at most 384 of the
+    // first 512 floats), then 384 zeros, the -delta a dead key's lane reads
     __shared__ __attribute__((aligned(16))) float qterms0[512 + 384];
     __shared__ __attribute__((aligned(16))) float qterms1[512 + 384];
-    // thirds 1 and 2's dK / dV sums of a row: [third - 1][key group][float4 j][lane]
-    __shared__ __attribute__((aligned(16))) float4 red[2 * 4 * 4 * 64];
+    // parts 1 .. kParts - 1's dK / dV sums of a row: [part - 1][key group][float4 j][lane]
+    __shared__ __attribute__((aligned(16))) float4 red[(kParts - 1) * 4 * 4 * 64];
 
     const int item = xcd_item(blockIdx.x, gridDim.x);
     const int rest = fdiv(item, a.fkb), kblk = item - rest * a.kblocks;
@@ -1184,7 +1198,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     const int rows = min(a.N, n_begin + a.chunk) - n_begin;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int kg = wave & 3, q3 = wave >> 2;
+    const int kg = wave & 3, q3 = wave >> 2;  // key group, query part
     const int r16 = lane & 15, g = lane >> 4;
     const int klocal = kg * 16 + r16;
     const int key = kblk * 64 + klocal;
@@ -1193,8 +1207,10 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
 
     if (tid < 192) reinterpret_cast<float4*>(tid < 96 ? qterms0 + 512 : qterms1 + 128)[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    // this wave's staging share of a step: tile (third sq3, tile si) of tensor (Q, dO)
-    const int ti = wave >> 1, tensor = wave & 1, sq3 = ti >> 1, si = ti & 1;
+    // this wave's staging share of a step: tile (part sq3, tile si) of tensor (Q, dO); waves past
+    // the step's kParts kTPS tiles x 2 tensors stage none
+    const int ti = wave >> 1, tensor = wave & 1, sq3 = ti / kTPS, si = ti % kTPS;
+    const bool stager = 2 * kTPS >= 4 || wave < 2 * kParts * kTPS;
     // as two direct-to-LDS loads of 16 LDS rows each: slot l of load i is LDS row R = 16 i + l / 4,
     // position p = l % 4, which holds chunk p ^ ((R / 4) % 4) of tile row x (perm_row(x, 8) = R)
     uint32_t dvoff[2];
@@ -1204,9 +1220,9 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
         const int x = 8 * ((R >> 2) & 3) + 4 * (R >> 4) + (R & 3);
         dvoff[i] = (uint32_t)((x * DP + 8 * (p ^ ((R >> 2) & 3))) * 2);
     }
-    const int dst_off = (2 * sq3 + si) * kSub + tensor * kOs;
+    const int dst_off = (kTPS * sq3 + si) * kSub + tensor * kOs;
     const half_t* const csrc = tensor ? a.dout : a.q;
-    // waves 0 and 1 stage the query terms: flat lane L < 96, tile L / 16 of [third][tile]
+    // the first waves stage the query terms: flat lane L < kQTerms, tile L / 16 of [part][tile]
     const int qL = wave * kWave + lane;
     const int qt_t = qL >> 4;
     const uint32_t qt_f = (uint32_t)(4 * (qL & 15));
@@ -1214,25 +1230,27 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     const auto row_n = [&](int pass) -> int { return n_begin + (pass < rows ? pass : 0); };
     const auto row_nh = [&](int pass) -> int64_t { return (int64_t)row_n(pass) * a.H + h; };
     // step `step` of row `pass` into LDS buffer buf, by direct-to-LDS loads: this wave's tile, and
-    // (waves 0 and 1) the step's query terms, lane qL to float 4 qL of the buffer's terms (wave 1's
-    // lanes 32..63 write zeros into its unused tail)
+    // (the first waves) the step's query terms, lane qL to float 4 qL of the buffer's terms (lanes
+    // past kQTerms write zeros into its unused tail)
     const auto dma_s = [&](int pass, int step, int buf) {
         const int64_t nh = row_nh(pass);
-        const int q0 = 32 * (sq3 * TT + 2 * step + si);
-        const auto rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<half_t*>(csrc + (nh * a.Sq + q0) * DP), 0, max(a.Sq - q0, 0) * DP * 2, 0x00020000);
-        half_t* dst = (buf ? lds1 : lds0) + dst_off;
+        if (stager) {
+            const int q0 = 32 * (sq3 * TT + kTPS * step + si);
+            const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<half_t*>(csrc + (nh * a.Sq + q0) * DP), 0, max(a.Sq - q0, 0) * DP * 2, 0x00020000);
+            half_t* dst = (buf ? lds1 : lds0) + dst_off;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16, dvoff[i], 0, 0, 0);
-        if (wave < 2) {
-            const int tg = (qt_t >> 1) * TT + 2 * step + (qt_t & 1);
+            for (int i = 0; i < 2; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rs, (__attribute__((address_space(3))) void*)(dst + 512 * i), 16, dvoff[i], 0, 0, 0);
+        }
+        if (wave * kWave < kQTerms) {
+            const int tg = (qt_t / kTPS) * TT + kTPS * step + (qt_t % kTPS);
             const auto rq = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float*>(a.qstat + nh * a.SqA * 2), 0, a.SqA * 2 * 4, 0x00020000);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rq, (__attribute__((address_space(3))) void*)((buf ? qterms1 : qterms0) + 256 * wave), 16,
-                qL < 96 ? ((uint32_t)(64 * tg) + qt_f) * 4u : 0x80000000u, 0, 0, 0);
+                qL < kQTerms ? ((uint32_t)(64 * tg) + qt_f) * 4u : 0x80000000u, 0, 0, 0);
         }
     };
 
@@ -1266,11 +1284,11 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     // (after the first step's loads are issued, so that their latency and the bias loads' overlap)
     // the workgroup's bias, fp16: rows kblk 64 .. + 63 and the masked-logit row SkA
     {
-        constexpr int kFill = (65 * (SqB / 4) + 767) / 768;
+        constexpr int kFill = (65 * (SqB / 4) + kNT - 1) / kNT;
         const float* src = a.biast + (int64_t)h * (a.SkA + 1) * SqB;
 #pragma unroll
         for (int f = 0; f < kFill; ++f) {
-            const int idx = tid + 768 * f;
+            const int idx = tid + kNT * f;
             if (idx < 65 * (SqB / 4)) {
                 const int r = idx / (SqB / 4), c4 = idx - r * (SqB / 4);
                 const int srow = r < 64 ? kblk * 64 + r : a.SkA;
@@ -1290,7 +1308,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
         const half8 vop = alive ? vopn : bzero8();
         // a dead key's lane: the masked-logit bias row, and -delta from the zeroed area
         const half_t* const brow = bias_l + (alive ? klocal : 64) * kBRow + q3 * TT * 32 + 8 * g;
-        const int qtS = q3 * 128 + 8 * g;
+        const int qtS = q3 * kTPS * 64 + 8 * g;
         const int qtD = qtS + 32 + (alive ? 0 : 512);
         float4v accv[2], acck[2];
 #pragma unroll
@@ -1305,16 +1323,16 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
             const int par = st & 1;  // kSteps is even
             // the next step's tiles into the other buffer, whose last reads ended at the barrier
             dma_s(pass + (st + 1) / kSteps, (st + 1) % kSteps, par ^ 1);
-            const half_t* buf = (par ? lds1 : lds0) + q3 * 2 * kSub;
+            const half_t* buf = (par ? lds1 : lds0) + q3 * kTPS * kSub;
             const float* qtb = par ? qterms1 : qterms0;
             // The step's two tiles as a pipeline: tile 1's S and dP products run beside tile 0's
             // softmax, and tile 0's dV / dK products beside tile 1's, so that each wave has
             // matrix-core work in flight while it issues vector instructions.
-            float4v sacc[2][2], dp[2][2];
-            half8 bb[2], pb[2], dsb[2];
+            float4v sacc[kTPS][2], dp[kTPS][2];
+            half8 bb[kTPS], pb[kTPS], dsb[kTPS];
             // S and dP of tile i: the LDS reads and four MFMAs
             const auto sdp = [&](int i) __attribute__((always_inline)) {
-                const int u = 2 * st + i;
+                const int u = kTPS * st + i;
                 const half_t* Qs = buf + i * kSub;
                 const half_t* Os = Qs + kOs;
                 const int qo = 64 * i;
@@ -1340,7 +1358,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
                     const float dsf = pin_f32(p * dp[i][j >> 2][j & 3]);
                     pb[i][j] = (half_t)p;
                     dsb[i][j] = (half_t)dsf;
-                    if constexpr (DBIAS) dbias[2 * st + i][j] = pin_f32(dbias[2 * st + i][j] + dsf);
+                    if constexpr (DBIAS) dbias[kTPS * st + i][j] = pin_f32(dbias[kTPS * st + i][j] + dsf);
                 }
             };
             // dV^T += dO^T P and dK^T += Q^T dS of tile i (k-slots queries 8 g + j, read transposed)
@@ -1355,12 +1373,18 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
                     acck[db] = mfma16x16x32(qt, dsb[i], acck[db]);
                 }
             };
-            sdp(0);
-            sdp(1);
-            soft(0);
-            dvdk(0);
-            soft(1);
-            dvdk(1);
+            if constexpr (kTPS == 2) {
+                sdp(0);
+                sdp(1);
+                soft(0);
+                dvdk(0);
+                soft(1);
+                dvdk(1);
+            } else {
+                sdp(0);
+                soft(0);
+                dvdk(0);
+            }
 #ifdef CLK_REG3_SGB
             // tile 0's reads and products; tile 1's reads; tile 1's products each beside a quarter
             // of tile 0's softmax; tile 0's transposed reads; its dV / dK products each beside a
@@ -1397,7 +1421,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
         }
 
         if (q3 == 0 && kin) {
-            // third 0 + third 1 + third 2, then lane holds d = 8 g .. + 8 of its key
+            // part 0 + part 1 + ..., then lane holds d = 8 g .. + 8 of its key
             float ks[8], vs[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -1405,7 +1429,7 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
                 vs[j] = accv[j / 4][j & 3];
             }
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < kParts - 1; ++t) {
                 const float4* r = red + (t * 4 + kg) * 4 * 64 + lane;
                 const float4 k0 = r[0], k1 = r[64], v0 = r[128], v1 = r[192];
                 ks[0] += k0.x; ks[1] += k0.y; ks[2] += k0.z; ks[3] += k0.w;
@@ -1438,8 +1462,10 @@ __global__ __launch_bounds__(768, 3) void attn_bwd_dkdv_reg3_kernel(BwdArgs a) {
     }
 }
 
-template __global__ void attn_bwd_dkdv_reg3_kernel<true>(BwdArgs);
-template __global__ void attn_bwd_dkdv_reg3_kernel<false>(BwdArgs);
+template __global__ void attn_bwd_dkdv_reg3_kernel<12, true>(BwdArgs);
+template __global__ void attn_bwd_dkdv_reg3_kernel<12, false>(BwdArgs);
+template __global__ void attn_bwd_dkdv_reg3_kernel<8, true>(BwdArgs);
+template __global__ void attn_bwd_dkdv_reg3_kernel<8, false>(BwdArgs);
 
 // With more than one query window: dk = fp16(scale * sum of the windows' dK sums), dv = fp16(sum
 // of their dV sums), each summed in window order, four elements per thread (D % 4 == 0).
@@ -1629,7 +1655,7 @@ static BwdPlan plan_bwd(int device, int64_t N, int64_t H, int64_t Sq, int64_t Sk
     const int64_t qtiles = std::max<int64_t>((Sq + 31) / 32, 1);
     const int64_t Nr = std::max<int64_t>(N, 1);  // N == 0 plans one (empty) chunk
     if (D == 32 && qtiles <= 12) {
-        // the register-partial kernels: one workgroup of eight (QT 4, 8) or twelve (QT 12) waves
+        // the register-partial kernels: one workgroup of eight (QT 4), sixteen (QT 8) or twelve (QT 12) waves
         // per CU, one row per pass;
         // chunks trade rounds of workgroups against dbias partials to write and sum (one
         // partial weighs about H kblocks / 128 row passes)
@@ -1768,14 +1794,18 @@ static int launch_bwd(hipStream_t stream, const BwdArgs& a, const BwdPlan& p, bo
             hipLaunchKernelGGL((attn_bwd_dkdv_reg_kernel<QT_, false>), dim3((unsigned)g2), dim3(512), 0, stream, a); \
         }                                                                                        \
     }
-            CLK_DKDV_REG(4) CLK_DKDV_REG(8)
-            if (p.QT == 12) {
-                if (want_dbias) {
-                    hipLaunchKernelGGL((attn_bwd_dkdv_reg3_kernel<true>), dim3((unsigned)g2), dim3(768), 0, stream, a);
-                } else {
-                    hipLaunchKernelGGL((attn_bwd_dkdv_reg3_kernel<false>), dim3((unsigned)g2), dim3(768), 0, stream, a);
-                }
-            }
+            CLK_DKDV_REG(4)
+#define CLK_DKDV_PARTS(QT_)                                                                      \
+    if (p.QT == QT_) {                                                                           \
+        constexpr int kNT = PartTile<QT_>::kThreads;                                             \
+        if (want_dbias) {                                                                        \
+            hipLaunchKernelGGL((attn_bwd_dkdv_reg3_kernel<QT_, true>), dim3((unsigned)g2), dim3(kNT), 0, stream, a); \
+        } else {                                                                                 \
+            hipLaunchKernelGGL((attn_bwd_dkdv_reg3_kernel<QT_, false>), dim3((unsigned)g2), dim3(kNT), 0, stream, a); \
+        }                                                                                        \
+    }
+            CLK_DKDV_PARTS(8) CLK_DKDV_PARTS(12)
+#undef CLK_DKDV_PARTS
 #undef CLK_DKDV_REG
         }
     } else if (p.QG == 4) {
