@@ -276,6 +276,26 @@ def test_long_sequences_with_dbias(hip, n, h, sq, sk, d):
     assert np.abs(off[3]).max() == 0.0
 
 
+@pytest.mark.parametrize("sq,sk", [(120, 100), (129, 250), (256, 256), (257, 130), (384, 70)])
+def test_register_kernels_want_dbias(hip, sq, sk):
+    """The register dK/dV kernels (eight waves for Sq <= 128, sixteen for Sq <= 256, twelve for
+    Sq <= 384) with and without their dBias partial: dq, dk and dv are the same bits either way,
+    the dbias output is zero without want_dbias, and with it the results meet the oracle."""
+    plan = hip.attention_bwd_plan(2, 2, sq, sk, 32)
+    assert plan["registers"] == 1, plan
+    got, ref = run(hip, n=2, h=2, sq=sq, sk=sk, d=32, seed=5)
+    check(got, ref, "register sq=%d sk=%d" % (sq, sk))
+    q, k, v, bias, km, dout = inputs(2, 2, sq, sk, 32, 5)
+    scale = 32.0 ** -0.5
+    tq, tk, tv, tb, tm, tdo = dev(q, k, v, bias, km, dout)
+    out, lse = hip.attention_fwd(tq, tk, tv, tb, tm, scale)
+    on = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale))
+    off = host(*hip.attention_bwd(tq, tk, tv, tb, tm, out, tdo, lse, scale, want_dbias=False))
+    for name, x, y in zip(("dq", "dk", "dv"), on[:3], off[:3]):
+        assert np.array_equal(x, y), name + " changed when want_dbias was off"
+    assert np.abs(off[3]).max() == 0.0
+
+
 def test_repeat_bit_exact(hip):
     q, k, v, bias, km, dout = inputs(3, 4, 96, 96, 32, 0)
     scale = 32.0 ** -0.5
